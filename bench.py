@@ -1,0 +1,275 @@
+#!/usr/bin/env python3
+"""Benchmark of the global-decay scan on one MI355X.
+
+Workload (the metric's configuration): full-sequence decay scan, bf16 V and y,
+fp32 arithmetic, B=8 N=4096 H=12 D=64 (25.2 M elements, 100.66 MB of
+algorithmic traffic per launch: one read of V, one write of y).  A step is one
+launch of the scan over one batch; inputs are resident in HBM and the step
+rotates over enough (V, y) buffer sets (400 MB) that the 256 MB Infinity Cache
+cannot hold the working set between launches.
+
+Prints one JSON line.  Also measured (under "extras"): the box's copy
+bandwidth, the decode step (C3: 256 x 12 x 64, launch-latency bound) and the
+long-context scan (C4: B=1 N=65536 H=16 D=128 bf16).  The CPU baseline is the
+oracle's restatement of the reference's CPU path timed on the host cores.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "decay-scan HBM GB/s (% of peak) + tokens/sec, B=8 N=4096 H=12 Dh=64 bf16"
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, vendor peak
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--rotate", type=int, default=4, help="(V, y) buffer sets cycled through")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-extras", action="store_true")
+    return p.parse_args()
+
+
+def c2_lam(H: int, torch):
+    g = torch.Generator().manual_seed(1)
+    u = 0.5 + (0.9999 - 0.5) * torch.rand(H, generator=g, dtype=torch.float64)
+    lam = torch.sigmoid(torch.log(u / (1 - u)).float())
+    lam[H - 1] = 0.9999
+    return lam
+
+
+class ScanLauncher:
+    """Direct C-ABI launches (no Python tensor plumbing inside the timed loop)."""
+
+    def __init__(self, torch, kilat_amd, lam, sets, code):
+        from kilat_amd import _lib
+        from kilat_amd.triton_ops import _stream_ptr, _workspace
+
+        self.lib = _lib.load()
+        V0 = sets[0][0]
+        B, H, N, D = V0.shape
+        dev = V0.device
+        self.stream = _stream_ptr(dev)
+        nbytes = self.lib.kdecay_scan_workspace_bytes(B, H, N, D, code)
+        ws = _workspace(dev, self.stream, nbytes)
+        self.args = []
+        for V, y in sets:
+            self.args.append((
+                V.data_ptr(), code, _lib.strides4(V.stride()), y.data_ptr(), code, _lib.strides4(y.stride()),
+                lam.data_ptr(), None, None, B, H, N, D, 0,
+                ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, self.stream,
+            ))
+        self.fn = self.lib.kdecay_scan_fwd
+        self.rc = 0
+
+    def __call__(self, k: int) -> None:
+        self.rc |= self.fn(*self.args[k % len(self.args)])
+
+
+def time_region(torch, launch, steps: int, warmup: int):
+    """(region ms over `steps` launches, per-launch event durations in ms)."""
+    for k in range(warmup):
+        launch(k)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for k in range(steps):
+        launch(k)
+    t1.record()
+    torch.cuda.synchronize()
+    region = t0.elapsed_time(t1)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for k in range(steps):
+        evs[k][0].record()
+        launch(k)
+        evs[k][1].record()
+    torch.cuda.synchronize()
+    per = [a.elapsed_time(b) for a, b in evs]
+    return region, per
+
+
+def copy_bandwidth(torch, dev) -> float:
+    n = 128 * 1024 * 1024  # 256 MB of bf16 per buffer, 4 pairs rotated
+    bufs = [(torch.empty(n, dtype=torch.bfloat16, device=dev), torch.empty(n, dtype=torch.bfloat16, device=dev))
+            for _ in range(2)]
+    for a, b in bufs:
+        a.fill_(1.0)
+
+    def launch(k):
+        a, b = bufs[k % 2]
+        b.copy_(a)
+
+    region, _ = time_region(torch, launch, 20, 4)
+    return 2 * n * 2 * 20 / (region * 1e-3) / 1e9
+
+
+def bench_decode(torch, kilat_amd, dev, steps=500):
+    from kilat_amd import _lib
+
+    S, H, D = 256, 12, 64
+    g = torch.Generator(device=dev).manual_seed(2)
+    lam = c2_lam(H, torch).to(dev)
+    state = torch.randn(S, H, D, generator=g, device=dev)
+    v = torch.randn(S, H, D, generator=g, device=dev).to(torch.bfloat16)
+    tpos = torch.randint(1, 2049, (S,), generator=g, device=dev, dtype=torch.int32)
+    out = torch.empty(S, H, D, device=dev)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    args = (lam.data_ptr(), state.data_ptr(), v.data_ptr(), _lib.KDECAY_BF16, state.data_ptr(), out.data_ptr(),
+            _lib.KDECAY_F32, tpos.data_ptr(), 0, S, H, D, stream)
+    rc = [0]
+
+    def launch(k):
+        rc[0] |= lib.kdecay_step(*args)
+
+    region, per = time_region(torch, launch, steps, 20)
+    if rc[0]:
+        raise RuntimeError("kdecay_step failed")
+    us = region * 1e3 / steps
+    return {"config": "C3: 256 seqs x 12 heads x 64, bf16 v_t, fp32 state, per-sequence t_pos",
+            "us_per_step": round(us, 3), "kernel_us_events": round(statistics.median(per) * 1e3, 3),
+            "tokens_per_s": round(S / (us * 1e-6), 1),
+            "bytes_per_step": S * H * D * (4 + 2 + 4 + 4)}
+
+
+def bench_long(torch, kilat_amd, dev, steps=20):
+    B, H, N, D = 1, 16, 65536, 128
+    g = torch.Generator(device=dev).manual_seed(3)
+    u = 0.99 + (0.99999 - 0.99) * torch.rand(H, generator=torch.Generator().manual_seed(3), dtype=torch.float64)
+    lam = torch.sigmoid(torch.log(u / (1 - u)).float()).to(dev)
+    sets = [(torch.randn(B, H, N, D, generator=g, device=dev).to(torch.bfloat16),
+             torch.empty(B, H, N, D, dtype=torch.bfloat16, device=dev)) for _ in range(2)]
+    from kilat_amd import _lib
+
+    launch = ScanLauncher(torch, kilat_amd, lam, sets, _lib.KDECAY_BF16)
+    region, per = time_region(torch, launch, steps, 3)
+    if launch.rc:
+        raise RuntimeError("kdecay_scan_fwd failed")
+    nbytes = B * H * N * D * 4
+    kern = statistics.mean(per)
+    return {"config": "C4: B=1 N=65536 H=16 D=128 bf16", "ms_per_step": round(region / steps, 5),
+            "GBps": round(nbytes * steps / (region * 1e-3) / 1e9, 1),
+            "kernel_GBps": round(nbytes / (kern * 1e-3) / 1e9, 1),
+            "pct_of_peak": round(100 * nbytes / (kern * 1e-3) / 1e9 / HBM_PEAK_GBPS, 2),
+            "tokens_per_s": round(B * N / (region / steps * 1e-3), 1)}
+
+
+def cpu_baseline(torch, B, H, N, D):
+    """The oracle's torch restatement of the reference CPU path on the host cores."""
+    from oracle import decay_oracle as O
+
+    cores = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit():
+        cores = min(cores, int(env))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(1)
+    V = torch.randn(B, H, N, D, generator=g).to(torch.bfloat16).float()
+    lam = c2_lam(H, torch)
+    O.global_decay(lam, V[:, :, :64])  # warm-up
+    times = []
+    for _ in range(3):
+        t = time.perf_counter()
+        O.global_decay(lam, V)
+        times.append(time.perf_counter() - t)
+    sec = statistics.median(times)
+    nbytes = B * H * N * D * 4  # same algorithmic bytes as the GPU line (bf16 in + out)
+    return {"value": round(nbytes / sec / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"full workload B={B} N={N} H={H} D={D} (bf16-rounded V as fp32), median of 3 runs after a warm-up",
+            "seconds": round(sec, 4), "tokens_per_s": round(B * N / sec, 1)}
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the decay scan shards over (b, h) streams with no communication; see DESIGN.md)",
+              file=sys.stderr, flush=True)
+        return 2
+    import torch
+
+    import kilat_amd
+    from kilat_amd import _lib
+
+    dev = torch.device("cuda", 0)
+    B, H, N, D = 8, 12, 4096, 64
+    log(f"allocating {args.rotate} x (V, y) bf16 {B}x{H}x{N}x{D}")
+    g = torch.Generator(device=dev).manual_seed(1)
+    sets = [(torch.randn(B, H, N, D, generator=g, device=dev).to(torch.bfloat16),
+             torch.empty(B, H, N, D, dtype=torch.bfloat16, device=dev)) for _ in range(args.rotate)]
+    lam = c2_lam(H, torch).to(dev)
+    launch = ScanLauncher(torch, kilat_amd, lam, sets, _lib.KDECAY_BF16)
+    log(f"timing {args.steps} steps after {args.warmup} warm-up")
+    region, per = time_region(torch, launch, args.steps, args.warmup)
+    if launch.rc:
+        raise RuntimeError("kdecay_scan_fwd failed: " + _lib.load().kdecay_last_error_string().decode())
+    if kilat_amd.workspace_error(sets[0][0]):
+        raise RuntimeError("scan workspace reports a look-back fault")
+
+    nbytes = B * H * N * D * (2 + 2)
+    ms_step = region / args.steps
+    value = nbytes / (ms_step * 1e-3) / 1e9
+    kern_ms = statistics.mean(per)
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    log(f"region {ms_step * 1e3:.2f} us/step, per-launch events mean {kern_ms * 1e3:.2f} us "
+        f"median {statistics.median(per) * 1e3:.2f} us")
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "full-sequence global-decay scan, bf16 V/y, fp32 accumulate",
+                   "B": B, "N": N, "H": H, "D": D, "io_dtype": "bf16", "rotated_buffer_sets": args.rotate,
+                   "parallelism": "single GPU"},
+        "tokens_per_s": round(B * N / (ms_step * 1e-3), 1),
+        "pct_of_peak": round(100 * value / HBM_PEAK_GBPS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel_us": round(kern_ms * 1e3, 3), "algorithmic_bytes": nbytes},
+    }
+    extras = {}
+    if not args.no_extras:
+        log("copy bandwidth")
+        extras["copy_GBps"] = round(copy_bandwidth(torch, dev), 1)
+        del sets, launch
+        torch.cuda.empty_cache()
+        log("decode step C3")
+        extras["decode"] = bench_decode(torch, kilat_amd, dev)
+        log("long context C4")
+        extras["long_context"] = bench_long(torch, kilat_amd, dev)
+    result["extras"] = extras
+    if not args.no_cpu_baseline:
+        log("CPU baseline (oracle restatement of the reference CPU path)")
+        result["cpu_baseline"] = cpu_baseline(torch, B, H, N, D)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

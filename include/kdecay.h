@@ -1,0 +1,146 @@
+/*
+ * kdecay.h — C ABI of libkdecay.so, the gfx950 (MI355X) global-decay scan.
+ *
+ * The operation (per batch b, head h, channel d, position t):
+ *
+ *     s_t = lam_h * s_{t-1} + V_t                 (s_{-1} = init state, or 0)
+ *     z_t = (1 - lam_h^(t+1)) / ((1 - lam_h) + 1e-6)
+ *     y_t = s_t / z_t
+ *
+ * with t counted from `t_offset` (0 for a whole sequence).  This is the
+ * recurrence of the reference's CPU path
+ *     /root/reference/src/kilat/arc/triton_ops.py:232-247  (_cpu_global_decay)
+ * which is also what its Triton kernel approximates
+ *     /root/reference/src/kilat/arc/triton_ops.py:6-230    (flash_decay_fwd_kernel)
+ * and of the inline incremental update in the attention layer
+ *     /root/reference/src/kilat/arc/attention.py:344-360   (twin :710-717).
+ *
+ * Conventions of every entry point:
+ *   - returns 0 on success; a negative KDECAY_E* code for a rejected argument
+ *     (nothing was launched); a positive hipError_t if a HIP call failed.
+ *     kdecay_last_error_string() describes the last failure of the calling
+ *     thread.
+ *   - pointers are device pointers unless stated otherwise; strides are in
+ *     elements, never bytes.
+ *   - nothing is allocated and nothing is synchronised: work is enqueued on
+ *     `stream` (a hipStream_t; NULL is the legacy default stream).
+ *   - lam is float32 [H]: decay factors, already passed through the sigmoid
+ *     (the reference computes lam = sigmoid(log_lambda) in the caller,
+ *     attention.py:319).
+ */
+#ifndef KDECAY_H
+#define KDECAY_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of V, y, v_t and the step output. */
+enum {
+  KDECAY_F32 = 0,
+  KDECAY_BF16 = 1,
+  KDECAY_F16 = 2
+};
+
+/* Rejected-argument codes (negative). */
+enum {
+  KDECAY_EINVAL = -1,     /* null pointer where one is required, negative size */
+  KDECAY_EDTYPE = -2,     /* unsupported dtype code or dtype combination       */
+  KDECAY_ESHAPE = -3,     /* unsupported head dim D                            */
+  KDECAY_ELAYOUT = -4,    /* strides / alignment the vector path cannot take   */
+  KDECAY_EWORKSPACE = -5  /* workspace missing or smaller than required        */
+};
+
+/*
+ * Full-sequence scan.
+ * Replaces triton_global_decay(lam_scores, V) -> out
+ *   /root/reference/src/kilat/arc/triton_ops.py:249-330
+ * whose GPU branch launches flash_decay_fwd_kernel (:6-230) with V's and
+ * out's four strides (:324-330) into out = torch.empty_like(V) (:309).
+ *
+ *   V            [B,H,N,D] of v_dtype, strides v_strides[4]
+ *   out          [B,H,N,D] of out_dtype, strides out_strides[4]
+ *                (out_dtype == v_dtype reproduces the reference; F32 out for
+ *                 a BF16/F16 V is also accepted)
+ *   init_state   nullable; fp32 [B,H,D] contiguous: state before position 0
+ *                (chunked prefill).  NULL means zeros, as the reference.
+ *   final_state  nullable; fp32 [B,H,D] contiguous: receives s_{N-1}, the
+ *                unnormalised state the reference seeds its decode cache
+ *                with in a Python loop (attention.py:383-394, :722-727).
+ *   t_offset     absolute position of row 0 (enters z only); 0 for a whole
+ *                sequence.
+ *   workspace    device memory of kdecay_scan_workspace_bytes() bytes, zeroed
+ *                once by the caller before its first use.  The kernels keep it
+ *                consistent from launch to launch (a launch counter and a work
+ *                ticket live in its header), so it must not be shared by two
+ *                launches that can run at the same time (use one per stream).
+ *                It may be NULL when kdecay_scan_workspace_bytes() returns 0.
+ *
+ * Requirements of this (vector) path: D in {16,32,64,128,256}; d-stride 1;
+ * 16-byte aligned V and out; the other strides multiples of 16 bytes.
+ * Anything else returns KDECAY_ELAYOUT / KDECAY_ESHAPE without launching.
+ */
+int kdecay_scan_fwd(const void* V, int v_dtype, const int64_t* v_strides,
+                    void* out, int out_dtype, const int64_t* out_strides,
+                    const float* lam, const float* init_state,
+                    float* final_state, int64_t B, int64_t H, int64_t N,
+                    int64_t D, int64_t t_offset, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace kdecay_scan_fwd needs for this shape (0: none). */
+size_t kdecay_scan_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D,
+                                   int v_dtype);
+
+/*
+ * Straight sequential scan: one lane per (b,h,d) column walks all N
+ * positions.  Same arguments and results as kdecay_scan_fwd (any strides, any
+ * D in 1..1024), no workspace.  Slow; it is the structurally independent
+ * second implementation the parity tests cross-check the chunked scan with.
+ * Same reference interface as kdecay_scan_fwd.
+ */
+int kdecay_scan_fwd_sequential(const void* V, int v_dtype,
+                               const int64_t* v_strides, void* out,
+                               int out_dtype, const int64_t* out_strides,
+                               const float* lam, const float* init_state,
+                               float* final_state, int64_t B, int64_t H,
+                               int64_t N, int64_t D, int64_t t_offset,
+                               void* stream);
+
+/*
+ * Incremental (decode) step for a whole batch, one launch.
+ * Replaces the inline update
+ *   new_state = lam.view(1,H,1) * past_state + V_current
+ *   z_inc     = (1 - lam**(t_pos+1)) / (1 - lam + 1e-6)
+ *   out       = new_state / z_inc
+ *   /root/reference/src/kilat/arc/attention.py:344-360 (twin :710-717)
+ *
+ *   state_in   fp32 [B,H,D] contiguous (the cache's global_state, :68-70)
+ *   v_t        [B,H,D] contiguous of v_dtype (V_current, :343)
+ *   state_out  fp32 [B,H,D]; may alias state_in (in-place update)
+ *   out        [B,H,D] of out_dtype (F32 reproduces the reference's type
+ *              promotion; BF16/F16 are rounded once from fp32)
+ *   t_pos      nullable int32 [B]: position of each sequence's new token.
+ *              NULL uses t_pos_scalar for every sequence, as the reference
+ *              does (t_pos = past_latent_kv.shape[1], :357-358).
+ * new_state is bit-identical to the reference's: one fp32 multiply and one
+ * fp32 add, each rounded (never fused).
+ */
+int kdecay_step(const float* lam, const float* state_in, const void* v_t,
+                int v_dtype, float* state_out, void* out, int out_dtype,
+                const int32_t* t_pos, int64_t t_pos_scalar, int64_t B,
+                int64_t H, int64_t D, void* stream);
+
+/* Library version string, e.g. "kdecay 0.1.0 gfx950". */
+const char* kdecay_version(void);
+
+/* Message for the calling thread's last non-zero return ("" if none). */
+const char* kdecay_last_error_string(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KDECAY_H */

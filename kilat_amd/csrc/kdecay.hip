@@ -1,0 +1,733 @@
+// kdecay.hip — MI355X (gfx950) kernels and C ABI of the global-decay scan.
+//
+//   s_t = lam_h * s_{t-1} + V_t,   z_t = (1 - lam_h^(t+1)) / ((1 - lam_h) + 1e-6),   y_t = s_t / z_t
+//
+// Reference semantics: /root/reference/src/kilat/arc/triton_ops.py:232-247 (full
+// sequence) and /root/reference/src/kilat/arc/attention.py:344-360 (one decode
+// step).  Declarations and argument contracts: include/kdecay.h.
+//
+// Full-sequence scan (scan_chunked): one workgroup per chunk of L rows of one
+// (b,h) stream, all D channels.  Each lane owns R consecutive rows of one
+// 16-byte channel slice and keeps them in registers; the chunk is reduced by a
+// sequential pass per lane, a shuffle scan across the lanes of a wavefront and
+// an LDS fold across wavefronts.  Chunks of one stream are chained in a single
+// pass by decoupled look-back: every chunk publishes its aggregate, then its
+// inclusive prefix, as 64-bit words (tag << 32 | float bits), one word per
+// channel, so a reader needs no fence: the tag and the value arrive together.
+// Work tickets are handed out in stream-interleaved chunk order at workgroup
+// start, so a chunk only ever waits on chunks whose workgroups are already
+// running.  The inclusive prefix of chunk c is always the same left fold
+//     F(c) = lam^L * F(c-1) + agg(c)
+// whoever evaluates it, so results are bitwise reproducible run to run.
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "kdecay.h"
+
+// The reference rounds lam*s and (lam*s)+v separately (two torch ops).  Keep
+// every multiply and add separately rounded in this file.
+#pragma clang fp contract(off)
+
+namespace kd {
+
+// --------------------------------------------------------------------------
+// Element conversion
+// --------------------------------------------------------------------------
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(__bf16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x);
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ __bf16 from_f32<__bf16>(float x) { return (__bf16)x; }
+template <>
+__device__ __forceinline__ _Float16 from_f32<_Float16>(float x) { return (_Float16)x; }
+
+// 16 bytes of T -> 16/sizeof(T) floats.
+template <typename T>
+__device__ __forceinline__ void unpack16(const uint4& u, float* f);
+
+template <>
+__device__ __forceinline__ void unpack16<float>(const uint4& u, float* f) {
+  f[0] = __uint_as_float(u.x);
+  f[1] = __uint_as_float(u.y);
+  f[2] = __uint_as_float(u.z);
+  f[3] = __uint_as_float(u.w);
+}
+
+template <>
+__device__ __forceinline__ void unpack16<__bf16>(const uint4& u, float* f) {
+  const unsigned w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    f[2 * k] = __uint_as_float(w[k] << 16);
+    f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+  }
+}
+
+template <>
+__device__ __forceinline__ void unpack16<_Float16>(const uint4& u, float* f) {
+  const unsigned w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const f16x2 h = __builtin_bit_cast(f16x2, w[k]);
+    f[2 * k] = (float)h.x;
+    f[2 * k + 1] = (float)h.y;
+  }
+}
+
+__device__ __forceinline__ unsigned pack2(__bf16*, float a, float b) {
+  bf16x2 p;
+  p.x = (__bf16)a;
+  p.y = (__bf16)b;
+  return __builtin_bit_cast(unsigned, p);
+}
+__device__ __forceinline__ unsigned pack2(_Float16*, float a, float b) {
+  f16x2 p;
+  p.x = (_Float16)a;
+  p.y = (_Float16)b;
+  return __builtin_bit_cast(unsigned, p);
+}
+
+// Store N floats (N = 4 or 8) as N elements of T at p (16-byte aligned).
+template <typename T, int N>
+__device__ __forceinline__ void store_vec(T* p, const float* f) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int k = 0; k < N / 4; ++k) {
+      uint4 u;
+      u.x = __float_as_uint(f[4 * k]);
+      u.y = __float_as_uint(f[4 * k + 1]);
+      u.z = __float_as_uint(f[4 * k + 2]);
+      u.w = __float_as_uint(f[4 * k + 3]);
+      reinterpret_cast<uint4*>(p)[k] = u;
+    }
+  } else {
+    static_assert(N == 8, "2-byte outputs are stored 8 at a time");
+    uint4 u;
+    u.x = pack2((T*)nullptr, f[0], f[1]);
+    u.y = pack2((T*)nullptr, f[2], f[3]);
+    u.z = pack2((T*)nullptr, f[4], f[5]);
+    u.w = pack2((T*)nullptr, f[6], f[7]);
+    *reinterpret_cast<uint4*>(p) = u;
+  }
+}
+
+// --------------------------------------------------------------------------
+// Normaliser, exactly as the reference's torch expression evaluates it:
+//   z = (1.0 - lam ** (t+1)) / (1.0 - lam + 1e-6)
+// torch's pow(tensor, int scalar) returns lam for e == 1, lam*lam for e == 2,
+// (lam*lam)*lam for e == 3 and the float rounding of the double-precision
+// power otherwise; every other operation is one rounded fp32 op.
+// --------------------------------------------------------------------------
+__device__ __forceinline__ float pow_like_torch(float x, int64_t e) {
+  if (e == 1) return x;
+  if (e == 2) return x * x;
+  if (e == 3) return (x * x) * x;
+  if (e == 0) return 1.0f;
+  return (float)pow((double)x, (double)e);
+}
+
+__device__ __forceinline__ float z_of(float lam, int64_t t) {
+  const float num = 1.0f - pow_like_torch(lam, t + 1);
+  const float den = (1.0f - lam) + 1e-6f;
+  return num / den;
+}
+
+// --------------------------------------------------------------------------
+// Look-back words and the workspace header
+// --------------------------------------------------------------------------
+typedef unsigned long long u64;
+
+// Header words (first 256 bytes of the workspace).
+enum { HDR_TICKET = 0, HDR_DONE = 1, HDR_EPOCH = 2, HDR_ERROR = 3 };
+constexpr size_t kHeaderBytes = 256;
+
+// Tag of a word published in launch `epoch`: kind 0 = aggregate, 1 = inclusive.
+// Zeroed memory (tag 0) never matches a live tag.
+__device__ __forceinline__ unsigned tag_of(unsigned epoch, unsigned kind) {
+  return (((epoch & 0x3fffffffu) + 1u) << 1) | kind;
+}
+
+__device__ __forceinline__ void publish(u64* p, unsigned tag, float v) {
+  const u64 w = ((u64)tag << 32) | (u64)__float_as_uint(v);
+  __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ u64 peek(const u64* p) {
+  return __hip_atomic_load(const_cast<u64*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Polls before a look-back gives up (about a second): the kernel then exits
+// normally and flags the header instead of hanging.
+constexpr int kSpinLimit = 1 << 20;
+
+// Carry into chunk `c` (c >= 1) for one channel: F(c-1).  `col` points at this
+// stream's word of chunk 0 for the channel; chunk k's word is col[k * D].
+template <int W, int D>
+__device__ float look_back(const u64* col, int c, unsigned tag_agg, unsigned tag_inc,
+                           float mL, unsigned* hdr) {
+  for (int spin = 0;; ++spin) {
+    u64 w[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k) w[k] = (c - 1 - k >= 0) ? peek(col + (int64_t)(c - 1 - k) * D) : 0ull;
+    // Nearest inclusive word with only aggregates between it and chunk c.
+    int m = -1;
+    bool open = true;
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      if (open && c - 1 - k >= 0) {
+        const unsigned tag = (unsigned)(w[k] >> 32);
+        if (tag == tag_inc) {
+          m = k;
+          open = false;
+        } else if (tag != tag_agg) {
+          open = false;
+        }
+      } else {
+        open = false;
+      }
+    }
+    if (m >= 0) {
+      float carry = __uint_as_float((unsigned)w[m]);
+#pragma unroll
+      for (int k = W - 1; k >= 0; --k)
+        if (k < m) carry = mL * carry + __uint_as_float((unsigned)w[k]);
+      return carry;
+    }
+    if (spin >= kSpinLimit) {
+      __hip_atomic_store(hdr + HDR_ERROR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return 0.0f;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
+// --------------------------------------------------------------------------
+// Chunked single-pass scan
+// --------------------------------------------------------------------------
+struct ScanArgs {
+  const void* V;
+  void* out;
+  const float* lam;
+  const float* init;  // [B*H*D] or null
+  float* fin;         // [B*H*D] or null
+  int64_t vb, vh, vn; // element strides of V (d stride 1)
+  int64_t ob, oh, on; // element strides of out (d stride 1)
+  int64_t H, N, t_offset;
+  int nchunk;   // chunks per stream
+  int nstream;  // B*H
+  u64* flags;   // [nstream][nchunk][D] look-back words (null if nchunk == 1)
+  unsigned* hdr;
+};
+
+// TI/TO: element types of V / out.  LPR lanes cover one row (D = LPR * VW);
+// each lane owns R rows; NW wavefronts per workgroup; W = look-back window.
+template <typename TI, typename TO, int LPR, int R, int NW, int W>
+__global__ __launch_bounds__(NW * 64) void scan_chunked(ScanArgs a) {
+  constexpr int VW = 16 / (int)sizeof(TI);  // channels per lane
+  constexpr int D = LPR * VW;
+  constexpr int GW = 64 / LPR;  // row groups per wavefront
+  constexpr int G = NW * GW;    // row groups per chunk
+  constexpr int L = G * R;      // rows per chunk
+  constexpr int NT = NW * 64;
+  constexpr int DQ = (D + 63) / 64;
+  static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "LPR must divide 64");
+
+  __shared__ unsigned s_tk[2];
+  __shared__ float s_rz[L];      // 1 / z of each row of the chunk
+  __shared__ float s_pw[G + 1];  // lam^(R*k), k = 0..G
+  __shared__ float s_wt[NW][D];  // per-wavefront totals (zero carry in)
+  __shared__ float s_carry[D];   // F(chunk - 1)
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const bool multi = a.nchunk > 1;
+  const unsigned total = (unsigned)a.nchunk * (unsigned)a.nstream;
+
+  unsigned ticket = blockIdx.x, epoch = 0;
+  if (multi) {
+    if (tid == 0) {
+      s_tk[0] = __hip_atomic_fetch_add(a.hdr + HDR_TICKET, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_tk[1] = __hip_atomic_load(a.hdr + HDR_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    ticket = s_tk[0];
+    epoch = s_tk[1];
+  }
+  const bool valid = ticket < total;  // false only if the header was corrupted
+  if (!valid) ticket = 0;
+
+  const int chunk = (int)(ticket / (unsigned)a.nstream);
+  const int stream = (int)(ticket % (unsigned)a.nstream);
+  const int64_t b = stream / a.H;
+  const int64_t h = stream % a.H;
+  const int64_t row0 = (int64_t)chunk * L;
+  const bool last = chunk == a.nchunk - 1;
+  const float lam = a.lam[h];
+
+  const int ds = lane % LPR;  // channel slice
+  const int gw = lane / LPR;  // row group within the wavefront
+  const int g = wave * GW + gw;
+  const int64_t rbase = row0 + (int64_t)g * R;
+
+  // 1. Issue the loads of this lane's R rows.
+  uint4 raw[R];
+  {
+    const TI* vp = static_cast<const TI*>(a.V) + b * a.vb + h * a.vh + (int64_t)ds * VW + rbase * a.vn;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      if (valid && rbase + i < a.N)
+        raw[i] = *reinterpret_cast<const uint4*>(vp + (int64_t)i * a.vn);
+      else
+        raw[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+
+  // 2. Per-head tables, while the loads are in flight.
+  if (tid <= G) s_pw[tid] = pow_like_torch(lam, (int64_t)tid * R);
+  for (int r = tid; r < L; r += NT) {
+    if (row0 + r < a.N) s_rz[r] = 1.0f / z_of(lam, a.t_offset + row0 + r);
+  }
+
+  // 3. Sequential pass over the lane's rows (zero carry in).
+  float acc[VW];
+#pragma unroll
+  for (int j = 0; j < VW; ++j) acc[j] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    float v[VW];
+    unpack16<TI>(raw[i], v);
+#pragma unroll
+    for (int j = 0; j < VW; ++j) acc[j] = lam * acc[j] + v[j];
+  }
+  __syncthreads();  // s_pw, s_rz
+
+  // 4. Inclusive scan over the row groups of the wavefront (lanes LPR apart).
+#pragma unroll
+  for (int k = 1; k < GW; k <<= 1) {
+    const float m = s_pw[k];
+#pragma unroll
+    for (int j = 0; j < VW; ++j) {
+      const float o = __shfl_up(acc[j], k * LPR, 64);
+      if (gw >= k) acc[j] = m * o + acc[j];
+    }
+  }
+  float xin[VW];  // state before this lane's first row, zero carry into the wavefront
+#pragma unroll
+  for (int j = 0; j < VW; ++j) {
+    const float o = __shfl_up(acc[j], LPR, 64);
+    xin[j] = gw > 0 ? o : 0.0f;
+  }
+  if (gw == GW - 1) {
+#pragma unroll
+    for (int j = 0; j < VW; ++j) s_wt[wave][ds * VW + j] = acc[j];
+  }
+  __syncthreads();
+
+  // 5. State before this wavefront's first row, zero carry into the chunk.
+  const float mW = s_pw[GW];
+  float ew[VW];
+#pragma unroll
+  for (int j = 0; j < VW; ++j) ew[j] = 0.0f;
+  for (int w = 0; w < wave; ++w) {
+#pragma unroll
+    for (int j = 0; j < VW; ++j) ew[j] = mW * ew[j] + s_wt[w][ds * VW + j];
+  }
+
+  // 6. Carry into the chunk: wavefront 0 publishes and looks back.
+  if (wave == 0) {
+    const float mL = s_pw[G];
+    const unsigned tag_agg = tag_of(epoch, 0u), tag_inc = tag_of(epoch, 1u);
+#pragma unroll
+    for (int q = 0; q < DQ; ++q) {
+      const int d = lane + 64 * q;
+      if (d < D) {
+        float agg = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) agg = mW * agg + s_wt[w][d];
+        float carry = 0.0f;
+        u64* col = multi ? a.flags + (int64_t)stream * a.nchunk * D + d : nullptr;
+        if (chunk == 0) {
+          if (a.init) carry = a.init[(int64_t)stream * D + d];
+        } else if (valid) {
+          if (!last) publish(col + (int64_t)chunk * D, tag_agg, agg);
+          carry = look_back<W, D>(col, chunk, tag_agg, tag_inc, mL, a.hdr);
+        }
+        if (multi && !last && valid) publish(col + (int64_t)chunk * D, tag_inc, mL * carry + agg);
+        s_carry[d] = carry;
+      }
+    }
+  }
+  __syncthreads();
+
+  // 7. Re-run the lane's rows from its true start state and store y.
+  if (valid) {
+    const float mg = s_pw[g];
+    const float mgw = s_pw[gw];
+    float st[VW];
+#pragma unroll
+    for (int j = 0; j < VW; ++j) st[j] = mg * s_carry[ds * VW + j] + (mgw * ew[j] + xin[j]);
+    TO* op = static_cast<TO*>(a.out) + b * a.ob + h * a.oh + (int64_t)ds * VW + rbase * a.on;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      if (rbase + i < a.N) {
+        float v[VW], y[VW];
+        unpack16<TI>(raw[i], v);
+        const float rz = s_rz[g * R + i];
+#pragma unroll
+        for (int j = 0; j < VW; ++j) {
+          st[j] = lam * st[j] + v[j];
+          y[j] = st[j] * rz;
+        }
+        store_vec<TO, VW>(op + (int64_t)i * a.on, y);
+        if (a.fin && rbase + i == a.N - 1) {
+#pragma unroll
+          for (int j = 0; j < VW; ++j) a.fin[(int64_t)stream * D + ds * VW + j] = st[j];
+        }
+      }
+    }
+  } else if (tid == 0) {
+    __hip_atomic_store(a.hdr + HDR_ERROR, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  // 8. The last workgroup to finish rewinds the ticket and advances the epoch.
+  // Every workgroup's ticket RMW has returned before its done RMW is issued,
+  // and RMWs are performed at the device coherence point, so when done reaches
+  // total every ticket has been drawn.
+  if (multi && tid == 0) {
+    const unsigned d = __hip_atomic_fetch_add(a.hdr + HDR_DONE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (d == total - 1u) {
+      __hip_atomic_store(a.hdr + HDR_TICKET, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.hdr + HDR_DONE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.hdr + HDR_EPOCH, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// --------------------------------------------------------------------------
+// Sequential scan: one lane per (b,h,d) column, exact division.
+// --------------------------------------------------------------------------
+struct SeqArgs {
+  const void* V;
+  void* out;
+  const float* lam;
+  const float* init;
+  float* fin;
+  int64_t vs[4], os[4];
+  int64_t B, H, N, D, t_offset;
+};
+
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void scan_sequential(SeqArgs a) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= a.B * a.H * a.D) return;
+  const int64_t d = idx % a.D;
+  const int64_t bh = idx / a.D;
+  const int64_t h = bh % a.H;
+  const int64_t b = bh / a.H;
+  const float lam = a.lam[h];
+  const TI* vp = static_cast<const TI*>(a.V) + b * a.vs[0] + h * a.vs[1] + d * a.vs[3];
+  TO* op = static_cast<TO*>(a.out) + b * a.os[0] + h * a.os[1] + d * a.os[3];
+  float s = a.init ? a.init[idx] : 0.0f;
+  for (int64_t t = 0; t < a.N; ++t) {
+    s = lam * s + to_f32(vp[t * a.vs[2]]);
+    op[t * a.os[2]] = from_f32<TO>(s / z_of(lam, a.t_offset + t));
+  }
+  if (a.fin) a.fin[idx] = s;
+}
+
+// --------------------------------------------------------------------------
+// Decode step for the whole batch
+// --------------------------------------------------------------------------
+struct StepArgs {
+  const float* lam;
+  const float* s_in;
+  const void* v;
+  float* s_out;
+  void* out;
+  const int32_t* tpos;
+  int64_t tpos_scalar;
+  int64_t H, D, total;
+};
+
+template <typename TV, typename TO>
+__global__ __launch_bounds__(256) void decay_step(StepArgs a) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= a.total) return;
+  const int64_t bh = idx / a.D;
+  const int64_t h = bh % a.H;
+  const int64_t b = bh / a.H;
+  const float lam = a.lam[h];
+  const float s = a.s_in[idx];
+  const float v = to_f32(static_cast<const TV*>(a.v)[idx]);
+  const float ns = lam * s + v;  // two roundings (contraction is off)
+  const int64_t tp = a.tpos ? (int64_t)a.tpos[b] : a.tpos_scalar;
+  a.s_out[idx] = ns;
+  static_cast<TO*>(a.out)[idx] = from_f32<TO>(ns / z_of(lam, tp));
+}
+
+// Final state of an empty sequence: the initial state (or zeros).
+__global__ __launch_bounds__(256) void copy_state(const float* init, float* fin, int64_t n) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx < n) fin[idx] = init ? init[idx] : 0.0f;
+}
+
+// --------------------------------------------------------------------------
+// Host side
+// --------------------------------------------------------------------------
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_check(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail((int)e, "%s: %s", what, hipGetErrorString(e));
+  return 0;
+}
+
+int elem_size(int dt) { return dt == KDECAY_F32 ? 4 : 2; }
+bool dtype_ok(int dt) { return dt == KDECAY_F32 || dt == KDECAY_BF16 || dt == KDECAY_F16; }
+
+// Launch shape of the chunked scan: a chunk holds NW * 64 lanes x R rows x
+// 16 bytes = 32 KiB of input whatever the dtype and D.
+constexpr int kR = 8;
+constexpr int kNW = 4;
+constexpr int kW = 16;
+
+int64_t chunk_rows(int v_dtype, int64_t D) {
+  const int64_t vw = 16 / elem_size(v_dtype);
+  const int64_t lpr = D / vw;
+  return kNW * (64 / lpr) * kR;
+}
+
+bool head_dim_ok(int v_dtype, int64_t D) {
+  if (!(D == 16 || D == 32 || D == 64 || D == 128 || D == 256)) return false;
+  const int64_t vw = 16 / elem_size(v_dtype);
+  const int64_t lpr = D / vw;
+  return lpr >= 1 && lpr <= 64;
+}
+
+template <typename TI, typename TO, int D>
+int launch_chunked(const ScanArgs& a, int64_t grid, hipStream_t s) {
+  constexpr int VW = 16 / (int)sizeof(TI);
+  constexpr int LPR = D / VW;
+  hipLaunchKernelGGL((scan_chunked<TI, TO, LPR, kR, kNW, kW>), dim3((unsigned)grid), dim3(kNW * 64), 0, s, a);
+  return hip_check("scan_chunked launch");
+}
+
+template <typename TI, typename TO>
+int dispatch_d(const ScanArgs& a, int64_t D, int64_t grid, hipStream_t s) {
+  switch (D) {
+    case 16: return launch_chunked<TI, TO, 16>(a, grid, s);
+    case 32: return launch_chunked<TI, TO, 32>(a, grid, s);
+    case 64: return launch_chunked<TI, TO, 64>(a, grid, s);
+    case 128: return launch_chunked<TI, TO, 128>(a, grid, s);
+    case 256: return launch_chunked<TI, TO, 256>(a, grid, s);
+  }
+  return fail(KDECAY_ESHAPE, "unsupported head dim D=%lld", (long long)D);
+}
+
+template <typename TI, typename TO>
+int launch_seq(const SeqArgs& a, hipStream_t s) {
+  const int64_t n = a.B * a.H * a.D;
+  hipLaunchKernelGGL((scan_sequential<TI, TO>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
+  return hip_check("scan_sequential launch");
+}
+
+template <typename TV, typename TO>
+int launch_step(const StepArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((decay_step<TV, TO>), dim3((unsigned)((a.total + 255) / 256)), dim3(256), 0, s, a);
+  return hip_check("decay_step launch");
+}
+
+// Common argument checks of the two scan entry points.
+int check_scan_args(const void* V, int v_dtype, const int64_t* v_strides, const void* out, int out_dtype,
+                    const int64_t* out_strides, const float* lam, int64_t B, int64_t H, int64_t N,
+                    int64_t D) {
+  if (B < 0 || H < 0 || N < 0 || D < 0) return fail(KDECAY_EINVAL, "negative size");
+  if (!dtype_ok(v_dtype) || !dtype_ok(out_dtype))
+    return fail(KDECAY_EDTYPE, "unknown dtype code (v=%d out=%d)", v_dtype, out_dtype);
+  if (out_dtype != v_dtype && out_dtype != KDECAY_F32)
+    return fail(KDECAY_EDTYPE, "out dtype must equal V's dtype or be F32");
+  if (B * H * N * D == 0) return 0;
+  if (!V || !out || !lam || !v_strides || !out_strides) return fail(KDECAY_EINVAL, "null pointer argument");
+  return 0;
+}
+
+int empty_final_state(const float* init, float* fin, int64_t n, hipStream_t s) {
+  if (!fin || n == 0) return 0;
+  hipLaunchKernelGGL(copy_state, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, init, fin, n);
+  return hip_check("copy_state launch");
+}
+
+}  // namespace kd
+
+using namespace kd;
+
+extern "C" {
+
+const char* kdecay_version(void) { return "kdecay 0.1.0 gfx950"; }
+
+const char* kdecay_last_error_string(void) { return g_err; }
+
+size_t kdecay_scan_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
+  if (B <= 0 || H <= 0 || N <= 0 || !dtype_ok(v_dtype) || !head_dim_ok(v_dtype, D)) return 0;
+  const int64_t L = chunk_rows(v_dtype, D);
+  const int64_t nchunk = (N + L - 1) / L;
+  if (nchunk <= 1) return 0;
+  return kHeaderBytes + (size_t)(B * H * nchunk * D) * sizeof(u64);
+}
+
+int kdecay_scan_fwd(const void* V, int v_dtype, const int64_t* v_strides, void* out, int out_dtype,
+                    const int64_t* out_strides, const float* lam, const float* init_state,
+                    float* final_state, int64_t B, int64_t H, int64_t N, int64_t D, int64_t t_offset,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_scan_args(V, v_dtype, v_strides, out, out_dtype, out_strides, lam, B, H, N, D);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (B * H * D == 0) return 0;
+  if (N == 0) return empty_final_state(init_state, final_state, B * H * D, s);
+  if (!head_dim_ok(v_dtype, D))
+    return fail(KDECAY_ESHAPE, "head dim D=%lld not in {16,32,64,128,256}", (long long)D);
+
+  const int64_t vw_in = 16 / elem_size(v_dtype);
+  const int64_t vw_out = 16 / elem_size(out_dtype);
+  if (v_strides[3] != 1 || out_strides[3] != 1) return fail(KDECAY_ELAYOUT, "channel (d) stride must be 1");
+  if (((uintptr_t)V & 15u) || ((uintptr_t)out & 15u)) return fail(KDECAY_ELAYOUT, "V and out must be 16-byte aligned");
+  const int64_t sizes[3] = {B, H, N};
+  for (int k = 0; k < 3; ++k) {  // a size-1 dim's stride is never used
+    if (sizes[k] > 1 && (v_strides[k] % vw_in || out_strides[k] % vw_out))
+      return fail(KDECAY_ELAYOUT, "stride %d is not a multiple of 16 bytes", k);
+  }
+
+  const int64_t L = chunk_rows(v_dtype, D);
+  const int64_t nchunk = (N + L - 1) / L;
+  const int64_t nstream = B * H;
+  const int64_t grid = nchunk * nstream;
+  if (grid > 0x7fffffffLL || nchunk > 0x7fffffffLL || nstream > 0x7fffffffLL)
+    return fail(KDECAY_EINVAL, "problem too large (%lld chunks)", (long long)grid);
+  const size_t need = kdecay_scan_workspace_bytes(B, H, N, D, v_dtype);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(KDECAY_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+  if (need && ((uintptr_t)workspace & 255u)) return fail(KDECAY_EWORKSPACE, "workspace must be 256-byte aligned");
+
+  ScanArgs a;
+  a.V = V;
+  a.out = out;
+  a.lam = lam;
+  a.init = init_state;
+  a.fin = final_state;
+  a.vb = v_strides[0];
+  a.vh = v_strides[1];
+  a.vn = v_strides[2];
+  a.ob = out_strides[0];
+  a.oh = out_strides[1];
+  a.on = out_strides[2];
+  a.H = H;
+  a.N = N;
+  a.t_offset = t_offset;
+  a.nchunk = (int)nchunk;
+  a.nstream = (int)nstream;
+  a.hdr = need ? static_cast<unsigned*>(workspace) : nullptr;
+  a.flags = need ? reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes) : nullptr;
+
+  if (v_dtype == KDECAY_F32) return dispatch_d<float, float>(a, D, grid, s);
+  if (v_dtype == KDECAY_BF16) {
+    if (out_dtype == KDECAY_BF16) return dispatch_d<__bf16, __bf16>(a, D, grid, s);
+    return dispatch_d<__bf16, float>(a, D, grid, s);
+  }
+  if (out_dtype == KDECAY_F16) return dispatch_d<_Float16, _Float16>(a, D, grid, s);
+  return dispatch_d<_Float16, float>(a, D, grid, s);
+}
+
+int kdecay_scan_fwd_sequential(const void* V, int v_dtype, const int64_t* v_strides, void* out,
+                               int out_dtype, const int64_t* out_strides, const float* lam,
+                               const float* init_state, float* final_state, int64_t B, int64_t H,
+                               int64_t N, int64_t D, int64_t t_offset, void* stream) {
+  int rc = check_scan_args(V, v_dtype, v_strides, out, out_dtype, out_strides, lam, B, H, N, D);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (B * H * D == 0) return 0;
+  if (N == 0) return empty_final_state(init_state, final_state, B * H * D, s);
+  if (D > 1024) return fail(KDECAY_ESHAPE, "head dim D=%lld > 1024", (long long)D);
+  if ((B * H * D + 255) / 256 > 0x7fffffffLL) return fail(KDECAY_EINVAL, "problem too large");
+  SeqArgs a;
+  a.V = V;
+  a.out = out;
+  a.lam = lam;
+  a.init = init_state;
+  a.fin = final_state;
+  for (int k = 0; k < 4; ++k) {
+    a.vs[k] = v_strides[k];
+    a.os[k] = out_strides[k];
+  }
+  a.B = B;
+  a.H = H;
+  a.N = N;
+  a.D = D;
+  a.t_offset = t_offset;
+  if (v_dtype == KDECAY_F32) return launch_seq<float, float>(a, s);
+  if (v_dtype == KDECAY_BF16) {
+    if (out_dtype == KDECAY_BF16) return launch_seq<__bf16, __bf16>(a, s);
+    return launch_seq<__bf16, float>(a, s);
+  }
+  if (out_dtype == KDECAY_F16) return launch_seq<_Float16, _Float16>(a, s);
+  return launch_seq<_Float16, float>(a, s);
+}
+
+int kdecay_step(const float* lam, const float* state_in, const void* v_t, int v_dtype, float* state_out,
+                void* out, int out_dtype, const int32_t* t_pos, int64_t t_pos_scalar, int64_t B, int64_t H,
+                int64_t D, void* stream) {
+  if (B < 0 || H < 0 || D < 0) return fail(KDECAY_EINVAL, "negative size");
+  if (!dtype_ok(v_dtype) || !dtype_ok(out_dtype))
+    return fail(KDECAY_EDTYPE, "unknown dtype code (v=%d out=%d)", v_dtype, out_dtype);
+  const int64_t total = B * H * D;
+  if (total == 0) return 0;
+  if (!lam || !state_in || !v_t || !state_out || !out) return fail(KDECAY_EINVAL, "null pointer argument");
+  if ((total + 255) / 256 > 0x7fffffffLL) return fail(KDECAY_EINVAL, "problem too large");
+  StepArgs a;
+  a.lam = lam;
+  a.s_in = state_in;
+  a.v = v_t;
+  a.s_out = state_out;
+  a.out = out;
+  a.tpos = t_pos;
+  a.tpos_scalar = t_pos_scalar;
+  a.H = H;
+  a.D = D;
+  a.total = total;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (v_dtype * 3 + out_dtype) {
+    case KDECAY_F32 * 3 + KDECAY_F32: return launch_step<float, float>(a, s);
+    case KDECAY_F32 * 3 + KDECAY_BF16: return launch_step<float, __bf16>(a, s);
+    case KDECAY_F32 * 3 + KDECAY_F16: return launch_step<float, _Float16>(a, s);
+    case KDECAY_BF16 * 3 + KDECAY_F32: return launch_step<__bf16, float>(a, s);
+    case KDECAY_BF16 * 3 + KDECAY_BF16: return launch_step<__bf16, __bf16>(a, s);
+    case KDECAY_BF16 * 3 + KDECAY_F16: return launch_step<__bf16, _Float16>(a, s);
+    case KDECAY_F16 * 3 + KDECAY_F32: return launch_step<_Float16, float>(a, s);
+    case KDECAY_F16 * 3 + KDECAY_BF16: return launch_step<_Float16, __bf16>(a, s);
+    default: return launch_step<_Float16, _Float16>(a, s);
+  }
+}
+
+}  // extern "C"

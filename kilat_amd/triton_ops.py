@@ -1,0 +1,254 @@
+"""MI355X drop-in for ``kilat.arc.triton_ops`` — the global-decay path.
+
+``triton_global_decay(lam_scores, V)`` keeps the reference's name, argument
+order, output allocation and dtype
+(/root/reference/src/kilat/arc/triton_ops.py:249-330) and runs the gfx950
+chunked scan of libkdecay.so on torch's current stream.  ``decay_step`` is the
+reference's inline incremental update (/root/reference/src/kilat/arc/
+attention.py:344-360) as one launch for the whole batch.
+``global_decay_scan`` exposes the library's extensions: a carry-in state, the
+final unnormalised state (the decode-cache seed the reference computes in a
+Python loop, attention.py:383-394), a position offset for chunked prefill and
+an fp32 output for bf16/fp16 input.
+
+Only HIP tensors are accepted.  There is no CPU path here: a CPU tensor, or a
+missing libkdecay.so, raises.  (kilat_amd.integration keeps the reference's
+own CPU function for CPU tensors when it patches kilat.)
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple, Union
+
+import torch
+
+from . import _lib
+
+_DTYPE_CODE = {
+    torch.float32: _lib.KDECAY_F32,
+    torch.bfloat16: _lib.KDECAY_BF16,
+    torch.float16: _lib.KDECAY_F16,
+}
+
+# Head dims of the chunked (vector) kernels; others use the sequential kernel.
+VECTOR_HEAD_DIMS = (16, 32, 64, 128, 256)
+
+# One zero-initialised workspace per (device, stream); the kernels keep it
+# consistent from launch to launch, so it is never cleared again.
+_workspaces: dict = {}
+
+
+def _require_hip(t: torch.Tensor, name: str) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"kilat_amd: {name} must be a torch.Tensor")
+    if not t.is_cuda:
+        raise RuntimeError(
+            f"kilat_amd: {name} is on {t.device}; the kilat_amd decay kernels run on HIP devices only "
+            "(the reference's _cpu_global_decay serves CPU tensors)"
+        )
+
+
+def _dtype_code(t: torch.Tensor, name: str) -> int:
+    try:
+        return _DTYPE_CODE[t.dtype]
+    except KeyError:
+        raise TypeError(f"kilat_amd: {name} dtype {t.dtype} is not float32/bfloat16/float16") from None
+
+
+def _vector_layout_ok(t: torch.Tensor) -> bool:
+    """The chunked kernel's layout rule: d-stride 1, 16-byte rows and base."""
+    vw = 16 // t.element_size()
+    if t.data_ptr() % 16:
+        return False
+    if t.size(3) > 1 and t.stride(3) != 1:
+        return False
+    return all(t.size(k) == 1 or t.stride(k) % vw == 0 for k in range(3))
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _workspace(device: torch.device, stream: int, nbytes: int) -> Optional[torch.Tensor]:
+    if nbytes == 0:
+        return None
+    key = (device.index, stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def workspace_error(V: torch.Tensor) -> int:
+    """Error word of the workspace used for V's device and current stream.
+
+    0: no fault.  1: a look-back gave up waiting (the output is wrong).
+    2: a workgroup drew an impossible ticket.  Synchronises the stream.
+    """
+    ws = _workspaces.get((V.device.index, _stream_ptr(V.device)))
+    if ws is None:
+        return 0
+    return int(ws[12:16].view(torch.int32).item())
+
+
+def _lam32(lam: torch.Tensor, H: int, device: torch.device) -> torch.Tensor:
+    _require_hip(lam, "lam_scores")
+    if lam.numel() != H:
+        raise ValueError(f"kilat_amd: lam_scores has {lam.numel()} elements, V has {H} heads")
+    return lam.detach().reshape(H).to(device=device, dtype=torch.float32).contiguous()
+
+
+def global_decay_scan(
+    lam: torch.Tensor,
+    V: torch.Tensor,
+    *,
+    initial_state: Optional[torch.Tensor] = None,
+    return_final_state: bool = False,
+    t_offset: int = 0,
+    out: Optional[torch.Tensor] = None,
+    out_dtype: Optional[torch.dtype] = None,
+    algorithm: str = "chunked",
+) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
+    """y[b,h,t] = s[b,h,t] / z_t with s_t = lam_h * s_{t-1} + V[b,h,t].
+
+    lam: [H] (any float dtype; used as fp32).  V: [B,H,N,D] fp32/bf16/fp16, any
+    strides.  initial_state: [B,H,D] state before position 0 (default zeros).
+    t_offset: absolute position of row 0 (z uses t_offset + t).
+    Returns y ([B,H,N,D], dtype out_dtype or V.dtype, laid out like V), and
+    with return_final_state also s_{N-1} ([B,H,D] fp32).
+    algorithm: "chunked" (default) or "sequential" (the cross-check kernel).
+    """
+    _require_hip(V, "V")
+    if V.dim() != 4:
+        raise ValueError(f"kilat_amd: V must be [B,H,N,D], got shape {tuple(V.shape)}")
+    v_code = _dtype_code(V, "V")
+    B, H, N, D = V.shape
+    dev = V.device
+    lam32 = _lam32(lam, H, dev)
+    if out is None:
+        out = torch.empty_like(V, dtype=out_dtype or V.dtype)
+    else:
+        _require_hip(out, "out")
+        if out.shape != V.shape or out.device != dev:
+            raise ValueError("kilat_amd: out must have V's shape and device")
+    o_code = _dtype_code(out, "out")
+    if o_code != v_code and o_code != _lib.KDECAY_F32:
+        raise TypeError("kilat_amd: out dtype must be V's dtype or float32")
+    init32 = None
+    if initial_state is not None:
+        _require_hip(initial_state, "initial_state")
+        if tuple(initial_state.shape) != (B, H, D):
+            raise ValueError(f"kilat_amd: initial_state must be [B,H,D]={B, H, D}")
+        init32 = initial_state.detach().to(device=dev, dtype=torch.float32).contiguous()
+    final = torch.empty((B, H, D), dtype=torch.float32, device=dev) if return_final_state else None
+    if algorithm not in ("chunked", "sequential"):
+        raise ValueError(f"kilat_amd: unknown algorithm {algorithm!r}")
+
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        stream = _stream_ptr(dev)
+        init_p = init32.data_ptr() if init32 is not None else None
+        fin_p = final.data_ptr() if final is not None else None
+        if algorithm == "sequential" or D not in VECTOR_HEAD_DIMS:
+            rc = lib.kdecay_scan_fwd_sequential(
+                V.data_ptr(), v_code, _lib.strides4(V.stride()),
+                out.data_ptr(), o_code, _lib.strides4(out.stride()),
+                lam32.data_ptr(), init_p, fin_p, B, H, N, D, int(t_offset), stream,
+            )
+            _lib.check(rc, "kdecay_scan_fwd_sequential")
+        else:
+            Vk = V if _vector_layout_ok(V) else V.contiguous()
+            outk = out if _vector_layout_ok(out) else torch.empty(V.shape, dtype=out.dtype, device=dev)
+            nbytes = lib.kdecay_scan_workspace_bytes(B, H, N, D, v_code)
+            ws = _workspace(dev, stream, nbytes)
+            rc = lib.kdecay_scan_fwd(
+                Vk.data_ptr(), v_code, _lib.strides4(Vk.stride()),
+                outk.data_ptr(), o_code, _lib.strides4(outk.stride()),
+                lam32.data_ptr(), init_p, fin_p, B, H, N, D, int(t_offset),
+                ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
+                stream,
+            )
+            _lib.check(rc, "kdecay_scan_fwd")
+            if outk is not out:
+                out.copy_(outk)
+    if return_final_state:
+        return out, final
+    return out
+
+
+def triton_global_decay(lam_scores: torch.Tensor, V: torch.Tensor) -> torch.Tensor:
+    """Drop-in for kilat.arc.triton_ops.triton_global_decay (triton_ops.py:249-330).
+
+    lam_scores: [H] decay factors (sigmoid already applied, attention.py:319).
+    V: [B,H,N,D] on a HIP device.  Returns out = empty_like(V) filled with
+    out[:,:,t] = (sum_{j<=t} lam^(t-j) V[:,:,j]) / z_t, z_t as the reference's
+    CPU path computes it (triton_ops.py:245).  Enqueued on the current stream,
+    no host synchronisation, no autograd graph (as the reference's GPU path).
+    """
+    return global_decay_scan(lam_scores, V)
+
+
+def decay_step(
+    lam: torch.Tensor,
+    past_state: torch.Tensor,
+    v_t: torch.Tensor,
+    t_pos: Union[int, torch.Tensor],
+    *,
+    out: Optional[torch.Tensor] = None,
+    new_state: Optional[torch.Tensor] = None,
+    out_dtype: torch.dtype = torch.float32,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """One incremental step for the whole batch (attention.py:344-360).
+
+        new_state = lam.view(1,H,1) * past_state + v_t        (two roundings)
+        out       = new_state / ((1 - lam**(t_pos+1)) / (1 - lam + 1e-6))
+
+    past_state: [B,H,D] (used as fp32, as the reference's promotion makes it).
+    v_t: [B,H,D] fp32/bf16/fp16 (any view of [B,1,H*D] reshapes to it).
+    t_pos: int shared by the batch (the reference's cache length) or an int
+    tensor [B] of per-sequence positions.  new_state may be past_state itself
+    (in-place).  Returns (out [B,H,D] out_dtype, new_state [B,H,D] fp32).
+    """
+    _require_hip(past_state, "past_state")
+    if past_state.dim() != 3:
+        raise ValueError(f"kilat_amd: past_state must be [B,H,D], got {tuple(past_state.shape)}")
+    B, H, D = past_state.shape
+    dev = past_state.device
+    _require_hip(v_t, "v_t")
+    if v_t.numel() != B * H * D:
+        raise ValueError(f"kilat_amd: v_t has {v_t.numel()} elements, expected B*H*D={B * H * D}")
+    v_code = _dtype_code(v_t, "v_t")
+    vk = v_t.detach().reshape(B, H, D).contiguous()
+    lam32 = _lam32(lam, H, dev)
+    s_in = past_state.detach()
+    if s_in.dtype != torch.float32 or not s_in.is_contiguous():
+        s_in = s_in.to(torch.float32).contiguous()
+    if new_state is None:
+        new_state = torch.empty((B, H, D), dtype=torch.float32, device=dev)
+    elif new_state.dtype != torch.float32 or not new_state.is_contiguous() or tuple(new_state.shape) != (B, H, D):
+        raise ValueError("kilat_amd: new_state must be a contiguous float32 [B,H,D] tensor")
+    if out is None:
+        out = torch.empty((B, H, D), dtype=out_dtype, device=dev)
+    elif not out.is_contiguous() or out.numel() != B * H * D:
+        raise ValueError("kilat_amd: out must be contiguous with B*H*D elements")
+    o_code = _dtype_code(out, "out")
+    tpos_ptr, tpos_scalar, tpos_dev = None, 0, None
+    if isinstance(t_pos, torch.Tensor):
+        if t_pos.numel() != B:
+            raise ValueError(f"kilat_amd: t_pos tensor must have B={B} elements")
+        tpos_dev = t_pos.detach().reshape(B).to(device=dev, dtype=torch.int32).contiguous()
+        tpos_ptr = tpos_dev.data_ptr()
+    else:
+        tpos_scalar = int(t_pos)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        rc = lib.kdecay_step(
+            lam32.data_ptr(), s_in.data_ptr(), vk.data_ptr(), v_code,
+            new_state.data_ptr(), out.data_ptr(), o_code,
+            tpos_ptr, tpos_scalar, B, H, D, _stream_ptr(dev),
+        )
+    _lib.check(rc, "kdecay_step")
+    return out, new_state
+
+
+__all__ = ["triton_global_decay", "decay_step", "global_decay_scan", "workspace_error", "VECTOR_HEAD_DIMS"]

@@ -1,0 +1,72 @@
+"""Seeded synthetic inputs of the benchmark configurations, and error metrics.
+
+Config numbering follows the workloads the parity tests and bench.py use:
+  C1  fp32 op, B=2 N=1024 H=6 D=64, lam in [0.90, 0.999]
+  C2  bf16 scan, B=8 N=4096 H=12 D=64, lam in [0.5, 0.9999], one head 0.9999
+  C3  decode, 256 sequences x 12 heads x 64, random prefixes, 128 steps
+  C4  bf16 long scan, B=1 N=65536 H=16 D=128, lam in [0.99, 0.99999]
+"""
+from __future__ import annotations
+
+import torch
+
+
+def lam_from_uniform(u: torch.Tensor) -> torch.Tensor:
+    """lam = sigmoid(log_lambda) with log_lambda = logit(u), as the layer computes it."""
+    u = u.double()
+    log_lambda = torch.log(u / (1 - u)).float()
+    return torch.sigmoid(log_lambda)
+
+
+def lam_uniform(H: int, lo: float, hi: float, g: torch.Generator) -> torch.Tensor:
+    return lam_from_uniform(lo + (hi - lo) * torch.rand(H, generator=g, dtype=torch.float64))
+
+
+def c1_inputs(seed: int = 0, B=2, N=1024, H=6, D=64):
+    g = torch.Generator().manual_seed(seed)
+    V = torch.randn(B, H, N, D, generator=g, dtype=torch.float32)
+    lam = lam_uniform(H, 0.90, 0.999, g)
+    return lam, V
+
+
+def c2_inputs(seed: int = 1, B=8, N=4096, H=12, D=64):
+    g = torch.Generator().manual_seed(seed)
+    V = torch.randn(B, H, N, D, generator=g, dtype=torch.float32).to(torch.bfloat16)
+    lam = lam_uniform(H, 0.5, 0.9999, g)
+    lam[H - 1] = 0.9999  # fp32 0.99989998: the long-memory head
+    return lam, V
+
+
+def c4_inputs(seed: int = 3, B=1, N=65536, H=16, D=128):
+    g = torch.Generator().manual_seed(seed)
+    V = torch.randn(B, H, N, D, generator=g, dtype=torch.float32).to(torch.bfloat16)
+    lam = lam_uniform(H, 0.99, 0.99999, g)
+    return lam, V
+
+
+def c3_inputs(seed: int = 2, S=256, H=12, D=64, steps=128, max_prefix=2048):
+    """Prefix lengths, bf16 prefix values (list, one [1,H,L,D] each), lam, bf16 step inputs [steps,S,H,D]."""
+    g = torch.Generator().manual_seed(seed)
+    lam = lam_uniform(H, 0.5, 0.9999, g)
+    lengths = torch.randint(1, max_prefix + 1, (S,), generator=g)
+    prefixes = [torch.randn(1, H, int(L), D, generator=g).to(torch.bfloat16) for L in lengths]
+    v_steps = torch.randn(steps, S, H, D, generator=g).to(torch.bfloat16)
+    return lam, lengths, prefixes, v_steps
+
+
+def rel_err(y: torch.Tensor, ref: torch.Tensor) -> float:
+    """max over (b,h) streams of max|y - ref| / max|ref| (fp64, finite refs)."""
+    y = y.double().cpu()
+    ref = ref.double().cpu()
+    B, H = ref.shape[:2]
+    num = (y - ref).abs().reshape(B, H, -1).amax(-1)
+    den = ref.abs().reshape(B, H, -1).amax(-1).clamp_min(1e-30)
+    return float((num / den).max())
+
+
+def max_abs(y: torch.Tensor, ref: torch.Tensor) -> float:
+    return float((y.double().cpu() - ref.double().cpu()).abs().max())
+
+
+def algorithmic_bytes(B, H, N, D, in_bytes, out_bytes) -> int:
+    return B * H * N * D * (in_bytes + out_bytes)

@@ -1,0 +1,130 @@
+"""C ABI and host-side logic, without a GPU: the library loads into a torch
+process, exports every symbol include/kdecay.h declares, and rejects bad
+arguments before any HIP call.  No kernel is launched here."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from kilat_amd import _build, _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "kdecay.h")
+
+FAKE = 0x10000  # a 16-byte aligned non-null address; never dereferenced on the host
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kdecay_\w+)\s*\(", text)))
+
+
+def test_header_declarations_match_binding():
+    assert declared_symbols() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(kdecay_lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", _build.LIBRARY], capture_output=True, text=True, check=True)
+    exported = set(re.findall(r"\bT (kdecay_\w+)", out.stdout))
+    for sym in declared_symbols():
+        assert sym in exported, sym
+        assert getattr(kdecay_lib, sym) is not None
+
+
+def test_single_hip_runtime_in_process(kdecay_lib):
+    maps = open(f"/proc/{os.getpid()}/maps").read()
+    runtimes = {line.split()[-1] for line in maps.splitlines() if "libamdhip64" in line}
+    assert len(runtimes) == 1, runtimes
+
+
+def test_version(kdecay_lib):
+    v = kdecay_lib.kdecay_version().decode()
+    assert v.startswith("kdecay ") and "gfx950" in v
+
+
+def test_workspace_bytes(kdecay_lib):
+    ws = kdecay_lib.kdecay_scan_workspace_bytes
+    # bf16 D=64: 256-row chunks; 16 chunks x 96 streams x 64 words + header
+    assert ws(8, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + 8 * 12 * 16 * 64 * 8
+    assert ws(2, 6, 256, 64, _lib.KDECAY_BF16) == 0  # one chunk per stream
+    assert ws(2, 6, 1024, 64, _lib.KDECAY_F32) == 256 + 2 * 6 * 8 * 64 * 8  # 128-row chunks
+    assert ws(1, 16, 65536, 128, _lib.KDECAY_BF16) == 256 + 16 * 512 * 128 * 8
+    assert ws(2, 6, 1024, 48, _lib.KDECAY_BF16) == 0  # unsupported D
+
+
+def _scan(lib, v_dtype=_lib.KDECAY_BF16, out_dtype=None, D=64, N=4096, vstr=None, ostr=None,
+          V=FAKE, out=FAKE, ws=None, wsb=0):
+    out_dtype = v_dtype if out_dtype is None else out_dtype
+    B, H = 2, 3
+    vstr = vstr or (H * N * D, N * D, D, 1)
+    ostr = ostr or (H * N * D, N * D, D, 1)
+    return lib.kdecay_scan_fwd(V, v_dtype, _lib.strides4(vstr), out, out_dtype, _lib.strides4(ostr),
+                               FAKE, None, None, B, H, N, D, 0, ws, wsb, None)
+
+
+def test_scan_rejects_bad_arguments(kdecay_lib):
+    lib = kdecay_lib
+    assert _scan(lib, v_dtype=7) == _lib.KDECAY_EDTYPE
+    assert _scan(lib, v_dtype=_lib.KDECAY_BF16, out_dtype=_lib.KDECAY_F16) == _lib.KDECAY_EDTYPE
+    assert _scan(lib, D=48) == _lib.KDECAY_ESHAPE
+    assert _scan(lib, V=FAKE + 2) == _lib.KDECAY_ELAYOUT
+    assert _scan(lib, vstr=(3 * 4096 * 64, 4096 * 64, 64, 2)) == _lib.KDECAY_ELAYOUT
+    assert _scan(lib, vstr=(3 * 4096 * 64, 4096 * 64, 68, 1)) == _lib.KDECAY_ELAYOUT
+    assert _scan(lib, V=None) == _lib.KDECAY_EINVAL
+    assert _scan(lib) == _lib.KDECAY_EWORKSPACE  # 16 chunks per stream need a workspace
+    assert _scan(lib, ws=FAKE, wsb=100) == _lib.KDECAY_EWORKSPACE
+    assert "workspace" in lib.kdecay_last_error_string().decode()
+    rc = lib.kdecay_scan_fwd(FAKE, 0, _lib.strides4((1, 1, 1, 1)), FAKE, 0, _lib.strides4((1, 1, 1, 1)),
+                             FAKE, None, None, -1, 1, 1, 16, 0, None, 0, None)
+    assert rc == _lib.KDECAY_EINVAL
+
+
+def test_sequential_and_step_reject_bad_arguments(kdecay_lib):
+    lib = kdecay_lib
+    s4 = _lib.strides4((1, 1, 1, 1))
+    assert lib.kdecay_scan_fwd_sequential(FAKE, 9, s4, FAKE, 0, s4, FAKE, None, None, 1, 1, 1, 16, 0,
+                                          None) == _lib.KDECAY_EDTYPE
+    assert lib.kdecay_scan_fwd_sequential(FAKE, 0, s4, FAKE, 0, s4, FAKE, None, None, 1, 1, 1, 2048, 0,
+                                          None) == _lib.KDECAY_ESHAPE
+    assert lib.kdecay_step(FAKE, FAKE, FAKE, 5, FAKE, FAKE, 0, None, 0, 1, 1, 1, None) == _lib.KDECAY_EDTYPE
+    assert lib.kdecay_step(None, FAKE, FAKE, 0, FAKE, FAKE, 0, None, 0, 1, 1, 1, None) == _lib.KDECAY_EINVAL
+    assert lib.kdecay_step(FAKE, FAKE, FAKE, 0, FAKE, FAKE, 0, None, 0, -1, 1, 1, None) == _lib.KDECAY_EINVAL
+    # empty problems are valid no-ops
+    assert lib.kdecay_step(None, None, None, 0, None, None, 0, None, 0, 0, 12, 64, None) == 0
+
+
+def test_python_check_raises_with_library_message(kdecay_lib):
+    rc = _scan(kdecay_lib, D=48)
+    with pytest.raises(RuntimeError, match="head dim"):
+        _lib.check(rc, "kdecay_scan_fwd")
+
+
+def test_shim_refuses_cpu_tensors():
+    import kilat_amd
+
+    lam = torch.full((2,), 0.9)
+    V = torch.randn(1, 2, 8, 16)
+    with pytest.raises(RuntimeError, match="HIP"):
+        kilat_amd.triton_global_decay(lam, V)
+    with pytest.raises(RuntimeError, match="HIP"):
+        kilat_amd.decay_step(lam, torch.zeros(1, 2, 16), torch.zeros(1, 2, 16), 3)
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIBRARY", str(tmp_path / "libkdecay.so"))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        _lib.load()
+
+
+def test_ctypes_signatures_cover_header(kdecay_lib):
+    # every declared function has an explicit restype (a missing one would
+    # silently truncate size_t / pointer returns to int)
+    for sym in declared_symbols():
+        assert getattr(kdecay_lib, sym).restype in (ctypes.c_int, ctypes.c_size_t, ctypes.c_char_p), sym

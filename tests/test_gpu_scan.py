@@ -1,0 +1,241 @@
+"""GPU parity of the full-sequence scan (kdecay_scan_fwd via kilat_amd) against
+the CPU oracle, which restates /root/reference/src/kilat/arc/triton_ops.py:232-247.
+
+Tolerances (from the build's target):
+  fp32 V:       rel_err <= 1e-5, rel_err = max over (b,h) of max|y - ref| / max|ref|
+  bf16/fp16 V:  max|y - ref| <= 2e-2, fp32 accumulation (ref computed from the
+                same rounded inputs, output rounded once like the reference)
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import kilat_amd
+from kilat_amd import _lib
+from oracle import decay_oracle as O
+from tests.decay_cases import c1_inputs, c2_inputs, c4_inputs, lam_uniform, max_abs, rel_err
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def chunk_rows(dtype, D):
+    vw = 16 // torch.empty((), dtype=dtype).element_size()
+    return 4 * (64 // (D // vw)) * 8
+
+
+def gpu_scan(lam, V, dev, **kw):
+    print(f"  scan V{tuple(V.shape)} {V.dtype} {kw}", flush=True)
+    res = kilat_amd.global_decay_scan(lam.to(dev), V.to(dev), **kw)
+    torch.cuda.synchronize()
+    return res
+
+
+def assert_parity(y, ref, dtype, what=""):
+    if dtype == torch.float32:
+        e = rel_err(y, ref)
+        assert e <= 1e-5, f"{what}: rel_err {e:.3e} > 1e-5"
+    else:
+        e = max_abs(y, ref)
+        assert e <= 2e-2, f"{what}: max_abs {e:.3e} > 2e-2"
+
+
+@pytest.mark.parametrize("dname", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
+def test_scan_shapes(hip_device, kdecay_lib, dname, D):
+    dtype = DTYPES[dname]
+    L = chunk_rows(dtype, D)
+    g = torch.Generator().manual_seed(100 + D)
+    lam = lam_uniform(3, 0.5, 0.9999, g)
+    for N in sorted({1, 37, L - 1, L, L + 1, 3 * L + 5}):
+        V = torch.randn(2, 3, N, D, generator=g).to(dtype)
+        y, fin = gpu_scan(lam, V, hip_device, return_final_state=True)
+        ref, sref = O.scan(lam, V)
+        assert y.dtype == dtype and y.shape == V.shape
+        assert_parity(y, ref, dtype, f"N={N}")
+        assert rel_err(fin, sref) <= 1e-5, f"final state N={N}"
+
+
+def test_c1_fp32_full(hip_device, kdecay_lib):
+    lam, V = c1_inputs()
+    y = gpu_scan(lam, V, hip_device)
+    ref = O.global_decay(lam, V)
+    assert_parity(y, ref, torch.float32, "C1")
+
+
+def test_c2_bf16_full(hip_device, kdecay_lib):
+    lam, V = c2_inputs()
+    y, fin = gpu_scan(lam, V, hip_device, return_final_state=True)
+    ref, sref = O.scan(lam, V)
+    assert_parity(y, ref, torch.bfloat16, "C2")
+    assert rel_err(fin, sref) <= 1e-5
+    assert kilat_amd.workspace_error(V.to(hip_device)) == 0
+
+
+def test_c4_bf16_long_context(hip_device, kdecay_lib):
+    lam, V = c4_inputs()
+    y, fin = gpu_scan(lam, V, hip_device, return_final_state=True)
+    ref, sref = O.scan(lam, V)
+    assert_parity(y, ref, torch.bfloat16, "C4")
+    assert rel_err(fin, sref) <= 1e-5
+    # the carry crosses 512 chunks per stream: the last rows depend on all of them
+    assert max_abs(y[:, :, -4096:], ref[:, :, -4096:]) <= 2e-2
+
+
+def test_sequential_kernel_matches_oracle_bits(hip_device, kdecay_lib):
+    lam, V = c1_inputs(N=512)
+    y, fin = gpu_scan(lam, V, hip_device, return_final_state=True, algorithm="sequential")
+    ref, sref = O.scan(lam, V)
+    assert torch.equal(fin.cpu(), sref)  # the recurrence itself is bit-exact
+    yb = y.cpu().numpy().view(np.int32).astype(np.int64)
+    rb = ref.numpy().view(np.int32).astype(np.int64)
+    ulps = np.abs(yb - rb)
+    assert ulps.max() <= 1 and (ulps > 0).mean() < 1e-4  # z from pow() may round one ulp apart
+
+
+def test_chunked_is_deterministic(hip_device, kdecay_lib):
+    lam, V = c2_inputs(B=2, N=8192)
+    y1 = gpu_scan(lam, V, hip_device)
+    y2 = gpu_scan(lam, V, hip_device)
+    assert torch.equal(y1, y2)
+
+
+def test_chunked_vs_sequential_kernel(hip_device, kdecay_lib):
+    lam, V = c1_inputs(N=2000, D=32)
+    y = gpu_scan(lam, V, hip_device)
+    ys = gpu_scan(lam, V, hip_device, algorithm="sequential")
+    assert rel_err(y, ys) <= 1e-5
+
+
+def test_layout_fused_strided_view(hip_device, kdecay_lib):
+    """V as the (B,N,H*D) projection viewed as (B,H,N,D): no contiguous() copy."""
+    g = torch.Generator().manual_seed(7)
+    B, N, H, D = 2, 700, 6, 64
+    lam = lam_uniform(H, 0.8, 0.999, g)
+    flat = torch.randn(B, N, H * D, generator=g).to(torch.bfloat16).to(hip_device)
+    V = flat.view(B, N, H, D).transpose(1, 2)
+    assert not V.is_contiguous()
+    y = kilat_amd.triton_global_decay(lam.to(hip_device), V)
+    assert y.stride() == V.stride()  # empty_like keeps the layout
+    yc = kilat_amd.triton_global_decay(lam.to(hip_device), V.contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(y, yc)
+    assert_parity(y, O.global_decay(lam, V.cpu()), torch.bfloat16, "strided")
+
+
+def test_misaligned_and_odd_layouts(hip_device, kdecay_lib):
+    g = torch.Generator().manual_seed(8)
+    lam = lam_uniform(2, 0.5, 0.99, g)
+    base = torch.randn(2 * 2 * 300 * 32 + 1, generator=g)
+    V = base[1:].view(2, 2, 300, 32)  # 4-byte offset: not 16-byte aligned
+    y = gpu_scan(lam, V, hip_device)
+    assert_parity(y, O.global_decay(lam, V), torch.float32, "misaligned")
+    Vt = torch.randn(2, 2, 32, 300, generator=g).transpose(2, 3)  # d-stride != 1
+    y = gpu_scan(lam, Vt, hip_device)
+    assert_parity(y, O.global_decay(lam, Vt.contiguous()), torch.float32, "d-strided")
+
+
+def test_unsupported_head_dim_uses_sequential_kernel(hip_device, kdecay_lib):
+    g = torch.Generator().manual_seed(9)
+    lam = lam_uniform(2, 0.5, 0.99, g)
+    V = torch.randn(1, 2, 100, 48, generator=g)
+    y = gpu_scan(lam, V, hip_device)
+    assert_parity(y, O.global_decay(lam, V), torch.float32, "D=48")
+
+
+def test_fp32_output_for_bf16_input(hip_device, kdecay_lib):
+    lam, V = c2_inputs(B=1, N=3000, H=4)
+    y = gpu_scan(lam, V, hip_device, out_dtype=torch.float32)
+    ref, _ = O.scan(lam, V, out_dtype=torch.float32)
+    assert y.dtype == torch.float32
+    assert_parity(y, ref, torch.float32, "bf16->f32")
+
+
+@pytest.mark.parametrize("dname", ["f32", "bf16"])
+def test_chunked_prefill_with_carry(hip_device, kdecay_lib, dname):
+    dtype = DTYPES[dname]
+    lam, V = c1_inputs(B=2, N=1500, H=3, D=64)
+    V = V.to(dtype)
+    y, s = gpu_scan(lam, V, hip_device, return_final_state=True)
+    y1, s1 = gpu_scan(lam, V[:, :, :700], hip_device, return_final_state=True)
+    y2, s2 = gpu_scan(lam, V[:, :, 700:], hip_device, return_final_state=True, initial_state=s1, t_offset=700)
+    ref, sref = O.scan(lam, V)
+    assert_parity(torch.cat([y1, y2], 2), ref, dtype, "split")
+    assert rel_err(s2, sref) <= 1e-5 and rel_err(s, sref) <= 1e-5
+    r2, _ = O.scan(lam, V[:, :, 700:], init_state=s1.cpu(), t_offset=700)
+    assert_parity(y2, r2, dtype, "carry-in")
+
+
+def test_lambda_edges_match_oracle(hip_device, kdecay_lib):
+    g = torch.Generator().manual_seed(11)
+    lam = torch.tensor([0.0, 1.0, 0.5, 1e-30])
+    V = torch.randn(2, 4, 600, 16, generator=g)
+    V[0, 1, 0, :3] = 0.0
+    y = gpu_scan(lam, V, hip_device).cpu()
+    ref = O.global_decay(lam, V)
+    assert torch.equal(torch.isnan(y), torch.isnan(ref))
+    assert torch.equal(torch.isinf(y), torch.isinf(ref))
+    fin = torch.isfinite(ref)
+    assert rel_err(torch.where(fin, y, 0), torch.where(fin, ref, 0)) <= 1e-5
+
+
+def test_nan_propagates_like_oracle(hip_device, kdecay_lib):
+    lam, V = c1_inputs(B=1, N=900, H=2, D=64)
+    V[0, 1, 300, 5] = float("nan")
+    y = gpu_scan(lam, V, hip_device).cpu()
+    ref = O.global_decay(lam, V)
+    assert torch.equal(torch.isnan(y), torch.isnan(ref))
+    assert torch.isnan(y[0, 1, 300:, 5]).all() and torch.isfinite(y[0, 1, :300]).all()
+
+
+def test_triton_global_decay_signature(hip_device, kdecay_lib):
+    lam, V = c1_inputs(B=1, N=300, H=2, D=32)
+    y = kilat_amd.triton_global_decay(lam.to(hip_device), V.to(hip_device))
+    torch.cuda.synchronize()
+    assert y.dtype == V.dtype and y.shape == V.shape and y.device.type == "cuda"
+    assert_parity(y, O.global_decay(lam, V), torch.float32, "drop-in")
+    # lam in another float dtype is used as fp32
+    y2 = kilat_amd.triton_global_decay(lam.double().to(hip_device), V.to(hip_device))
+    assert torch.equal(y, y2)
+
+
+def test_empty_and_degenerate(hip_device, kdecay_lib):
+    lam = torch.tensor([0.9, 0.8]).to(hip_device)
+    V = torch.zeros(0, 2, 10, 16, device=hip_device)
+    assert kilat_amd.triton_global_decay(lam, V).shape == V.shape
+    V = torch.zeros(1, 2, 0, 16, device=hip_device)
+    init = torch.randn(1, 2, 16, device=hip_device)
+    y, fin = kilat_amd.global_decay_scan(lam, V, initial_state=init, return_final_state=True)
+    torch.cuda.synchronize()
+    assert y.shape == V.shape and torch.equal(fin, init)
+
+
+def test_golden_fixtures_on_gpu(hip_device, kdecay_lib):
+    import os
+
+    d = np.load(os.path.join(os.path.dirname(__file__), "golden", "decay_golden.npz"))
+
+    def t(name, bf16=False):
+        a = d[name]
+        if bf16:
+            return torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)
+        return torch.from_numpy(a.copy())
+
+    y, fin = gpu_scan(t("scan_f32_lam"), t("scan_f32_V"), hip_device, return_final_state=True)
+    assert_parity(y, t("scan_f32_out"), torch.float32, "golden f32")
+    assert rel_err(fin, t("scan_f32_final")) <= 1e-5
+    y, fin = gpu_scan(t("scan_bf16_lam"), t("scan_bf16_V", True), hip_device, return_final_state=True)
+    assert_parity(y, t("scan_bf16_out", True), torch.bfloat16, "golden bf16")
+    y, fin = gpu_scan(t("scan_init_lam"), t("scan_init_V"), hip_device, return_final_state=True,
+                      initial_state=t("scan_init_init").to(hip_device), t_offset=int(d["scan_init_offset"]))
+    assert_parity(y, t("scan_init_out"), torch.float32, "golden init")
+    assert rel_err(fin, t("scan_init_final")) <= 1e-5
+
+
+def test_workspace_clean_after_suite(hip_device, kdecay_lib):
+    lam, V = c2_inputs(B=1, N=5000, H=2)
+    gpu_scan(lam, V, hip_device)
+    assert kilat_amd.workspace_error(V.to(hip_device)) == 0

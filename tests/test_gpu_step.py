@@ -1,0 +1,118 @@
+"""GPU parity of the fused decode step (kdecay_step via kilat_amd.decay_step)
+against the oracle restatement of /root/reference/src/kilat/arc/attention.py:344-360.
+
+The state must match bit for bit after every step (fp32, same layout
+[B,H,D]); the normalised output too, except where the double-precision power
+inside z may round one ulp apart (checked as <= 1 ulp).
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import kilat_amd
+from oracle import c_oracle as C
+from oracle import decay_oracle as O
+from tests.decay_cases import c3_inputs, lam_uniform
+
+pytestmark = pytest.mark.gpu
+
+
+def ulps(a: torch.Tensor, b: torch.Tensor) -> np.ndarray:
+    x = a.detach().cpu().float().numpy().view(np.int32).astype(np.int64)
+    y = b.detach().cpu().float().numpy().view(np.int32).astype(np.int64)
+    return np.abs(x - y)
+
+
+def test_step_scalar_tpos_bitwise(hip_device, kdecay_lib):
+    g = torch.Generator().manual_seed(20)
+    lam = lam_uniform(6, 0.5, 0.9999, g)
+    state = torch.randn(8, 6, 64, generator=g) * 4
+    for tp in (0, 1, 2, 3, 4, 17, 1000, 65535):
+        v = torch.randn(8, 6, 64, generator=g).to(torch.bfloat16)
+        print(f"  step t_pos={tp}", flush=True)
+        out, ns = kilat_amd.decay_step(lam.to(hip_device), state.to(hip_device), v.to(hip_device), tp)
+        ro, rs = O.step(lam, state, v, tp)
+        torch.cuda.synchronize()
+        assert torch.equal(ns.cpu(), rs), tp
+        assert out.dtype == torch.float32 and ulps(out, ro).max() <= 1, tp
+        state = rs
+
+
+def test_c3_decode_128_steps_bitwise_state(hip_device, kdecay_lib):
+    lam, lengths, prefixes, v_steps = c3_inputs()
+    S, H, D = len(prefixes), lam.numel(), v_steps.shape[-1]
+    # prefixes pre-scanned on the CPU (C oracle: bit-equal to the torch restatement)
+    state = np.concatenate([C.scan_f32(lam.numpy(), p.float().numpy())[1] for p in prefixes], 0)
+    state = torch.from_numpy(state)
+    assert state.shape == (S, H, D)
+    dev_state = state.to(hip_device)
+    dev_lam = lam.to(hip_device)
+    worst = 0
+    for k in range(v_steps.shape[0]):
+        tpos = lengths + k
+        v = v_steps[k]
+        out, dev_state = kilat_amd.decay_step(dev_lam, dev_state, v.to(hip_device), tpos.to(hip_device))
+        ro, rs = C.step_f32(lam.numpy(), state.numpy(), v.float().numpy(), tpos.tolist())
+        if k == 0:  # the torch restatement gives the same bits (per-sequence positions)
+            ro_t, rs_t = O.step(lam, state, v, tpos.tolist())
+            assert torch.equal(rs_t, torch.from_numpy(rs)) and torch.equal(ro_t, torch.from_numpy(ro))
+        torch.cuda.synchronize()
+        rs = torch.from_numpy(rs)
+        assert torch.equal(dev_state.cpu(), rs), f"state differs at step {k}"
+        worst = max(worst, int(ulps(out, torch.from_numpy(ro)).max()))
+        state = rs
+    assert worst <= 1
+
+
+def test_step_in_place_and_out_dtypes(hip_device, kdecay_lib):
+    g = torch.Generator().manual_seed(21)
+    lam = lam_uniform(4, 0.5, 0.999, g).to(hip_device)
+    s0 = torch.randn(3, 4, 32, generator=g).to(hip_device)
+    v = torch.randn(3, 4, 32, generator=g).to(hip_device)
+    out_ref, ns_ref = kilat_amd.decay_step(lam, s0, v, 9)
+    s = s0.clone()
+    out, ns = kilat_amd.decay_step(lam, s, v, 9, new_state=s)
+    torch.cuda.synchronize()
+    assert ns.data_ptr() == s.data_ptr() and torch.equal(s, ns_ref) and torch.equal(out, out_ref)
+    ob, _ = kilat_amd.decay_step(lam, s0, v, 9, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(ob, out_ref.to(torch.bfloat16))
+
+
+def test_step_golden_fixture(hip_device, kdecay_lib):
+    d = np.load(os.path.join(os.path.dirname(__file__), "golden", "decay_golden.npz"))
+    lam = torch.from_numpy(d["step_lam"].copy())
+    state = torch.from_numpy(d["step_state"].copy())
+    v = torch.from_numpy(d["step_v"].view(np.int16).copy()).view(torch.bfloat16)
+    out, ns = kilat_amd.decay_step(lam.to(hip_device), state.to(hip_device), v.to(hip_device),
+                                   int(d["step_tpos_scalar"]))
+    torch.cuda.synchronize()
+    assert torch.equal(ns.cpu(), torch.from_numpy(d["step_new_state"]))
+    assert ulps(out, torch.from_numpy(d["step_out"])).max() <= 1
+    tp = torch.from_numpy(d["step_tpos"].astype(np.int32)).to(hip_device)
+    out, ns = kilat_amd.decay_step(lam.to(hip_device), state.to(hip_device), v.to(hip_device), tp)
+    torch.cuda.synchronize()
+    assert torch.equal(ns.cpu(), torch.from_numpy(d["step_new_state_vec"]))
+    assert ulps(out, torch.from_numpy(d["step_out_vec"])).max() <= 1
+
+
+def test_scan_then_steps_continue_the_sequence(hip_device, kdecay_lib):
+    """Prefill with the scan's final state, then decode: equals one longer scan."""
+    g = torch.Generator().manual_seed(22)
+    lam = lam_uniform(3, 0.5, 0.999, g)
+    V = torch.randn(2, 3, 520, 64, generator=g)
+    dev = hip_device
+    _, s = kilat_amd.global_decay_scan(lam.to(dev), V[:, :, :500].to(dev), return_final_state=True)
+    outs = []
+    for t in range(500, 520):
+        o, s = kilat_amd.decay_step(lam.to(dev), s, V[:, :, t].to(dev), t)
+        outs.append(o)
+    torch.cuda.synchronize()
+    ref, sref = O.scan(lam, V)
+    y = torch.stack(outs, 2).cpu()
+    assert float(((y - ref[:, :, 500:]).abs().amax() / ref[:, :, 500:].abs().amax())) <= 1e-5
+    assert float(((s.cpu() - sref).abs().amax() / sref.abs().amax())) <= 1e-5
