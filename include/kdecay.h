@@ -72,12 +72,18 @@ enum {
  *                with in a Python loop (attention.py:383-394, :722-727).
  *   t_offset     absolute position of row 0 (enters z only); 0 for a whole
  *                sequence.
- *   workspace    device memory of kdecay_scan_workspace_bytes() bytes, zeroed
- *                once by the caller before its first use.  The kernels keep it
- *                consistent from launch to launch (a launch counter and a work
- *                ticket live in its header), so it must not be shared by two
- *                launches that can run at the same time (use one per stream).
- *                It may be NULL when kdecay_scan_workspace_bytes() returns 0.
+ *   workspace    device memory of kdecay_scan_workspace_bytes() bytes,
+ *                256-byte aligned, zeroed once by the caller before its first
+ *                use.  It holds the look-back words of the chunks and a
+ *                header (launch epoch, a count of finished streams, a sticky
+ *                error word).  Each launch advances the epoch on the device,
+ *                so the workspace needs no clearing between launches (also
+ *                under stream capture and graph replay), but it must not be
+ *                shared by two launches that can run at the same time (use
+ *                one per stream).  A non-zero error word (header word 2: a
+ *                look-back gave up waiting, and that launch's output is
+ *                wrong) stays set until the caller zeroes the workspace.  It
+ *                may be NULL when kdecay_scan_workspace_bytes() returns 0.
  *
  * Requirements of this (vector) path: D in {16,32,64,128,256}; d-stride 1;
  * 16-byte aligned V and out; the other strides multiples of 16 bytes.

@@ -14,9 +14,9 @@
 // pass by decoupled look-back: every chunk publishes its aggregate, then its
 // inclusive prefix, as 64-bit words (tag << 32 | float bits), one word per
 // channel, so a reader needs no fence: the tag and the value arrive together.
-// Work tickets are handed out in stream-interleaved chunk order at workgroup
-// start, so a chunk only ever waits on chunks whose workgroups are already
-// running.  The inclusive prefix of chunk c is always the same left fold
+// Workgroups are numbered chunk-major, so a chunk only waits on workgroups
+// with smaller indices.  The inclusive prefix of chunk c is always the same
+// left fold
 //     F(c) = lam^L * F(c-1) + agg(c)
 // whoever evaluates it, so results are bitwise reproducible run to run.
 
@@ -101,43 +101,56 @@ __device__ __forceinline__ unsigned pack2(_Float16*, float a, float b) {
   return __builtin_bit_cast(unsigned, p);
 }
 
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte store of data written once and not read back by this kernel
+// (non-temporal: it does not displace cached data).
+__device__ __forceinline__ void store16_stream(void* p, unsigned a, unsigned b, unsigned c, unsigned d) {
+  const u32x4 v = {a, b, c, d};
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
 // Store N floats (N = 4 or 8) as N elements of T at p (16-byte aligned).
 template <typename T, int N>
 __device__ __forceinline__ void store_vec(T* p, const float* f) {
   if constexpr (sizeof(T) == 4) {
 #pragma unroll
-    for (int k = 0; k < N / 4; ++k) {
-      uint4 u;
-      u.x = __float_as_uint(f[4 * k]);
-      u.y = __float_as_uint(f[4 * k + 1]);
-      u.z = __float_as_uint(f[4 * k + 2]);
-      u.w = __float_as_uint(f[4 * k + 3]);
-      reinterpret_cast<uint4*>(p)[k] = u;
-    }
+    for (int k = 0; k < N / 4; ++k)
+      store16_stream(p + 4 * k, __float_as_uint(f[4 * k]), __float_as_uint(f[4 * k + 1]),
+                     __float_as_uint(f[4 * k + 2]), __float_as_uint(f[4 * k + 3]));
   } else {
     static_assert(N == 8, "2-byte outputs are stored 8 at a time");
-    uint4 u;
-    u.x = pack2((T*)nullptr, f[0], f[1]);
-    u.y = pack2((T*)nullptr, f[2], f[3]);
-    u.z = pack2((T*)nullptr, f[4], f[5]);
-    u.w = pack2((T*)nullptr, f[6], f[7]);
-    *reinterpret_cast<uint4*>(p) = u;
+    store16_stream(p, pack2((T*)nullptr, f[0], f[1]), pack2((T*)nullptr, f[2], f[3]),
+                   pack2((T*)nullptr, f[4], f[5]), pack2((T*)nullptr, f[6], f[7]));
   }
 }
 
 // --------------------------------------------------------------------------
-// Normaliser, exactly as the reference's torch expression evaluates it:
+// Normaliser, as the reference's torch expression evaluates it:
 //   z = (1.0 - lam ** (t+1)) / (1.0 - lam + 1e-6)
 // torch's pow(tensor, int scalar) returns lam for e == 1, lam*lam for e == 2,
-// (lam*lam)*lam for e == 3 and the float rounding of the double-precision
-// power otherwise; every other operation is one rounded fp32 op.
+// (lam*lam)*lam for e == 3, and a float power otherwise.  For e >= 4 this
+// takes the float rounding of lam^e evaluated in double by binary
+// exponentiation (at most 2*64 double products, relative error < 2^-45, so
+// the float result is the correctly rounded power except within 2^-45 of a
+// rounding tie).  Every other operation is one rounded fp32 op.
 // --------------------------------------------------------------------------
+__device__ __forceinline__ double ipow_f64(double x, int64_t e) {
+  double r = 1.0;
+  while (e > 0) {
+    if (e & 1) r *= x;
+    x *= x;
+    e >>= 1;
+  }
+  return r;
+}
+
 __device__ __forceinline__ float pow_like_torch(float x, int64_t e) {
   if (e == 1) return x;
   if (e == 2) return x * x;
   if (e == 3) return (x * x) * x;
   if (e == 0) return 1.0f;
-  return (float)pow((double)x, (double)e);
+  return (float)ipow_f64((double)x, e);
 }
 
 __device__ __forceinline__ float z_of(float lam, int64_t t) {
@@ -152,7 +165,10 @@ __device__ __forceinline__ float z_of(float lam, int64_t t) {
 typedef unsigned long long u64;
 
 // Header words (first 256 bytes of the workspace).
-enum { HDR_TICKET = 0, HDR_DONE = 1, HDR_EPOCH = 2, HDR_ERROR = 3 };
+//   EPOCH  launch generation: look-back words of older launches never match
+//   DONE   streams of the running launch whose last chunk has finished
+//   ERROR  sticky fault word (1: a look-back gave up waiting)
+enum { HDR_EPOCH = 0, HDR_DONE = 1, HDR_ERROR = 2 };
 constexpr size_t kHeaderBytes = 256;
 
 // Tag of a word published in launch `epoch`: kind 0 = aggregate, 1 = inclusive.
@@ -170,35 +186,28 @@ __device__ __forceinline__ u64 peek(const u64* p) {
   return __hip_atomic_load(const_cast<u64*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Polls before a look-back gives up (about a second): the kernel then exits
-// normally and flags the header instead of hanging.
-constexpr int kSpinLimit = 1 << 20;
+// Polls before a look-back gives up (well over a second): the kernel then
+// exits normally and flags the header instead of hanging.
+constexpr int kSpinLimit = 1 << 21;
 
-// Carry into chunk `c` (c >= 1) for one channel: F(c-1).  `col` points at this
-// stream's word of chunk 0 for the channel; chunk k's word is col[k * D].
+// Carry into chunk `c` (c >= 1) for one channel: F(c-1), the inclusive prefix
+// of the chunk before.  `col` points at this stream's word of chunk 0 for the
+// channel; chunk k's word is col[k * D].  Reads the W nearest predecessors at
+// once and folds the aggregates after the nearest inclusive word.
 template <int W, int D>
-__device__ float look_back(const u64* col, int c, unsigned tag_agg, unsigned tag_inc,
-                           float mL, unsigned* hdr) {
+__device__ float look_back(const u64* col, int c, unsigned tag_agg, unsigned tag_inc, float mL,
+                           unsigned* hdr) {
   for (int spin = 0;; ++spin) {
     u64 w[W];
 #pragma unroll
     for (int k = 0; k < W; ++k) w[k] = (c - 1 - k >= 0) ? peek(col + (int64_t)(c - 1 - k) * D) : 0ull;
-    // Nearest inclusive word with only aggregates between it and chunk c.
     int m = -1;
     bool open = true;
 #pragma unroll
     for (int k = 0; k < W; ++k) {
-      if (open && c - 1 - k >= 0) {
-        const unsigned tag = (unsigned)(w[k] >> 32);
-        if (tag == tag_inc) {
-          m = k;
-          open = false;
-        } else if (tag != tag_agg) {
-          open = false;
-        }
-      } else {
-        open = false;
-      }
+      const unsigned tag = (unsigned)(w[k] >> 32);
+      if (open && c - 1 - k >= 0 && tag == tag_inc) m = k;
+      if (c - 1 - k < 0 || tag != tag_agg) open = false;
     }
     if (m >= 0) {
       float carry = __uint_as_float((unsigned)w[m]);
@@ -211,7 +220,7 @@ __device__ float look_back(const u64* col, int c, unsigned tag_agg, unsigned tag
       __hip_atomic_store(hdr + HDR_ERROR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return 0.0f;
     }
-    __builtin_amdgcn_s_sleep(2);
+    __builtin_amdgcn_s_sleep(1);
   }
 }
 
@@ -233,161 +242,187 @@ struct ScanArgs {
   unsigned* hdr;
 };
 
+// 16-byte load of data read exactly once (non-temporal: no cache residency).
+__device__ __forceinline__ uint4 load16_stream(const void* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Keeps `x` opaque to the optimiser at this point, so values derived from it
+// are recomputed after the barrier rather than held in registers across it.
+__device__ __forceinline__ void opaque(uint4& x) {
+  asm volatile("" : "+v"(x.x), "+v"(x.y), "+v"(x.z), "+v"(x.w));
+}
+
+// One chunk ("item") of the scan: L rows x D channels of one (b,h) stream.
 // TI/TO: element types of V / out.  LPR lanes cover one row (D = LPR * VW);
-// each lane owns R rows; NW wavefronts per workgroup; W = look-back window.
+// each lane owns R consecutive rows of one 16-byte channel slice; NW
+// wavefronts per workgroup; W = look-back window.
+//
+// Items are numbered chunk-major (item = chunk * nstream + stream), so the
+// chunk an item waits on always has a smaller item number.
 template <typename TI, typename TO, int LPR, int R, int NW, int W>
-__global__ __launch_bounds__(NW * 64) void scan_chunked(ScanArgs a) {
-  constexpr int VW = 16 / (int)sizeof(TI);  // channels per lane
-  constexpr int D = LPR * VW;
-  constexpr int GW = 64 / LPR;  // row groups per wavefront
-  constexpr int G = NW * GW;    // row groups per chunk
-  constexpr int L = G * R;      // rows per chunk
-  constexpr int NT = NW * 64;
-  constexpr int DQ = (D + 63) / 64;
+struct ChunkScan {
+  static constexpr int VW = 16 / (int)sizeof(TI);  // channels per lane
+  static constexpr int D = LPR * VW;
+  static constexpr int GW = 64 / LPR;  // row groups per wavefront
+  static constexpr int G = NW * GW;    // row groups per chunk
+  static constexpr int L = G * R;      // rows per chunk
+  static constexpr int NT = NW * 64;
+  static constexpr int DQ = (D + 63) / 64;
   static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "LPR must divide 64");
+  static_assert(G + 1 <= NT, "power table is filled one entry per thread");
 
-  __shared__ unsigned s_tk[2];
-  __shared__ float s_rz[L];      // 1 / z of each row of the chunk
-  __shared__ float s_pw[G + 1];  // lam^(R*k), k = 0..G
-  __shared__ float s_wt[NW][D];  // per-wavefront totals (zero carry in)
-  __shared__ float s_carry[D];   // F(chunk - 1)
+  struct Smem {
+    float rz[L];      // 1 / z of each row of the chunk
+    float pw[G + 1];  // lam^(R*k), k = 0..G
+    float wt[NW][D];  // per-wavefront totals (zero carry in)
+    float carry[D];   // F(chunk - 1)
+  };
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const bool multi = a.nchunk > 1;
-  const unsigned total = (unsigned)a.nchunk * (unsigned)a.nstream;
-
-  unsigned ticket = blockIdx.x, epoch = 0;
-  if (multi) {
-    if (tid == 0) {
-      s_tk[0] = __hip_atomic_fetch_add(a.hdr + HDR_TICKET, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_tk[1] = __hip_atomic_load(a.hdr + HDR_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    ticket = s_tk[0];
-    epoch = s_tk[1];
-  }
-  const bool valid = ticket < total;  // false only if the header was corrupted
-  if (!valid) ticket = 0;
-
-  const int chunk = (int)(ticket / (unsigned)a.nstream);
-  const int stream = (int)(ticket % (unsigned)a.nstream);
-  const int64_t b = stream / a.H;
-  const int64_t h = stream % a.H;
-  const int64_t row0 = (int64_t)chunk * L;
-  const bool last = chunk == a.nchunk - 1;
-  const float lam = a.lam[h];
-
-  const int ds = lane % LPR;  // channel slice
-  const int gw = lane / LPR;  // row group within the wavefront
-  const int g = wave * GW + gw;
-  const int64_t rbase = row0 + (int64_t)g * R;
-
-  // 1. Issue the loads of this lane's R rows.
-  uint4 raw[R];
-  {
-    const TI* vp = static_cast<const TI*>(a.V) + b * a.vb + h * a.vh + (int64_t)ds * VW + rbase * a.vn;
+  // Issue the loads of this lane's R rows of `item`.  Rows past the end of
+  // the sequence read row N-1 instead: the loads stay unconditional (a load
+  // under a branch gets a full memory wait at the branch join, serialising
+  // the R loads), and rows past the end only ever feed later rows past the
+  // end and the last chunk's aggregate, which is never published.
+  //
+  // Returns the item's decay factor, loaded first: memory operations retire
+  // in issue order, so its first use then waits for it alone, not for the
+  // rows, and the per-head tables are computed while the rows are in flight.
+  __device__ static float load(const ScanArgs& a, int item, uint4 (&raw)[R]) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int chunk = item / a.nstream, stream = item % a.nstream;
+    const int64_t b = stream / a.H, h = stream % a.H;
+    const float lam = a.lam[h];
+    const int ds = lane % LPR, gw = lane / LPR;
+    const int64_t rbase = (int64_t)chunk * L + (int64_t)(wave * GW + gw) * R;
+    const TI* vp = static_cast<const TI*>(a.V) + b * a.vb + h * a.vh + (int64_t)ds * VW;
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      if (valid && rbase + i < a.N)
-        raw[i] = *reinterpret_cast<const uint4*>(vp + (int64_t)i * a.vn);
-      else
-        raw[i] = make_uint4(0u, 0u, 0u, 0u);
+      const int64_t r = rbase + i < a.N ? rbase + i : a.N - 1;
+      raw[i] = load16_stream(vp + r * a.vn);
     }
+    return lam;
   }
 
-  // 2. Per-head tables, while the loads are in flight.
-  if (tid <= G) s_pw[tid] = pow_like_torch(lam, (int64_t)tid * R);
-  for (int r = tid; r < L; r += NT) {
-    if (row0 + r < a.N) s_rz[r] = 1.0f / z_of(lam, a.t_offset + row0 + r);
-  }
+  // Scan `item` from its loaded rows and store its outputs.  `epoch` is the
+  // launch generation every workgroup read before publishing anything.
+  __device__ static void process(const ScanArgs& a, int item, uint4 (&raw)[R], float lam, unsigned epoch,
+                                 Smem& sm) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool multi = a.nchunk > 1;
+    const int chunk = item / a.nstream, stream = item % a.nstream;
+    const int64_t b = stream / a.H, h = stream % a.H;
+    const int64_t row0 = (int64_t)chunk * L;
+    const bool last = chunk == a.nchunk - 1;
+    const int ds = lane % LPR, gw = lane / LPR;
+    const int g = wave * GW + gw;
+    const int64_t rbase = row0 + (int64_t)g * R;
 
-  // 3. Sequential pass over the lane's rows (zero carry in).
-  float acc[VW];
-#pragma unroll
-  for (int j = 0; j < VW; ++j) acc[j] = 0.0f;
-#pragma unroll
-  for (int i = 0; i < R; ++i) {
-    float v[VW];
-    unpack16<TI>(raw[i], v);
-#pragma unroll
-    for (int j = 0; j < VW; ++j) acc[j] = lam * acc[j] + v[j];
-  }
-  __syncthreads();  // s_pw, s_rz
-
-  // 4. Inclusive scan over the row groups of the wavefront (lanes LPR apart).
-#pragma unroll
-  for (int k = 1; k < GW; k <<= 1) {
-    const float m = s_pw[k];
-#pragma unroll
-    for (int j = 0; j < VW; ++j) {
-      const float o = __shfl_up(acc[j], k * LPR, 64);
-      if (gw >= k) acc[j] = m * o + acc[j];
+    // Per-head tables.  The barrier keeps them from being overwritten while
+    // the previous item of this workgroup still reads them.
+    __syncthreads();
+    if (tid <= G) sm.pw[tid] = pow_like_torch(lam, (int64_t)tid * R);
+    for (int r = tid; r < L; r += NT) {
+      if (row0 + r < a.N) sm.rz[r] = 1.0f / z_of(lam, a.t_offset + row0 + r);
     }
-  }
-  float xin[VW];  // state before this lane's first row, zero carry into the wavefront
-#pragma unroll
-  for (int j = 0; j < VW; ++j) {
-    const float o = __shfl_up(acc[j], LPR, 64);
-    xin[j] = gw > 0 ? o : 0.0f;
-  }
-  if (gw == GW - 1) {
-#pragma unroll
-    for (int j = 0; j < VW; ++j) s_wt[wave][ds * VW + j] = acc[j];
-  }
-  __syncthreads();
 
-  // 5. State before this wavefront's first row, zero carry into the chunk.
-  const float mW = s_pw[GW];
-  float ew[VW];
+    // Sequential pass over the lane's rows (zero carry in).
+    float acc[VW];
 #pragma unroll
-  for (int j = 0; j < VW; ++j) ew[j] = 0.0f;
-  for (int w = 0; w < wave; ++w) {
+    for (int j = 0; j < VW; ++j) acc[j] = 0.0f;
 #pragma unroll
-    for (int j = 0; j < VW; ++j) ew[j] = mW * ew[j] + s_wt[w][ds * VW + j];
-  }
+    for (int i = 0; i < R; ++i) {
+      float v[VW];
+      unpack16<TI>(raw[i], v);
+#pragma unroll
+      for (int j = 0; j < VW; ++j) acc[j] = lam * acc[j] + v[j];
+    }
+    __syncthreads();  // tables
 
-  // 6. Carry into the chunk: wavefront 0 publishes and looks back.
-  if (wave == 0) {
-    const float mL = s_pw[G];
-    const unsigned tag_agg = tag_of(epoch, 0u), tag_inc = tag_of(epoch, 1u);
+    // Inclusive scan over the row groups of the wavefront (lanes LPR apart).
 #pragma unroll
-    for (int q = 0; q < DQ; ++q) {
-      const int d = lane + 64 * q;
-      if (d < D) {
-        float agg = 0.0f;
+    for (int k = 1; k < GW; k <<= 1) {
+      const float m = sm.pw[k];
 #pragma unroll
-        for (int w = 0; w < NW; ++w) agg = mW * agg + s_wt[w][d];
-        float carry = 0.0f;
-        u64* col = multi ? a.flags + (int64_t)stream * a.nchunk * D + d : nullptr;
-        if (chunk == 0) {
-          if (a.init) carry = a.init[(int64_t)stream * D + d];
-        } else if (valid) {
-          if (!last) publish(col + (int64_t)chunk * D, tag_agg, agg);
-          carry = look_back<W, D>(col, chunk, tag_agg, tag_inc, mL, a.hdr);
-        }
-        if (multi && !last && valid) publish(col + (int64_t)chunk * D, tag_inc, mL * carry + agg);
-        s_carry[d] = carry;
+      for (int j = 0; j < VW; ++j) {
+        const float o = __shfl_up(acc[j], k * LPR, 64);
+        if (gw >= k) acc[j] = m * o + acc[j];
       }
     }
-  }
-  __syncthreads();
+    if (gw == GW - 1) {
+#pragma unroll
+      for (int j = 0; j < VW; ++j) sm.wt[wave][ds * VW + j] = acc[j];
+    }
+    // State before this lane's first row, zero carry into the wavefront.
+#pragma unroll
+    for (int j = 0; j < VW; ++j) {
+      const float o = __shfl_up(acc[j], LPR, 64);
+      acc[j] = gw > 0 ? o : 0.0f;
+    }
+    __syncthreads();
 
-  // 7. Re-run the lane's rows from its true start state and store y.
-  if (valid) {
-    const float mg = s_pw[g];
-    const float mgw = s_pw[gw];
+    // Carry into the chunk: wavefront 0 publishes and looks back.
+    const float mW = sm.pw[GW];
+    if (wave == 0) {
+      const float mL = sm.pw[G];
+      const unsigned tag_agg = tag_of(epoch, 0u), tag_inc = tag_of(epoch, 1u);
+#pragma unroll
+      for (int q = 0; q < DQ; ++q) {
+        const int d = lane + 64 * q;
+        if (d < D) {
+          float agg = 0.0f;
+#pragma unroll
+          for (int w = 0; w < NW; ++w) agg = mW * agg + sm.wt[w][d];
+          float carry = 0.0f;
+          u64* col = multi ? a.flags + (int64_t)stream * a.nchunk * D + d : nullptr;
+          if (chunk == 0) {
+            if (a.init) carry = a.init[(int64_t)stream * D + d];
+          } else {
+            if (!last) publish(col + (int64_t)chunk * D, tag_agg, agg);
+            carry = look_back<W, D>(col, chunk, tag_agg, tag_inc, mL, a.hdr);
+          }
+          if (multi && !last) publish(col + (int64_t)chunk * D, tag_inc, mL * carry + agg);
+          sm.carry[d] = carry;
+        }
+      }
+    }
+    __syncthreads();
+
+    // The last chunk of a stream has seen, through its look-back, a word of
+    // every earlier chunk of the stream, each written after its workgroup
+    // read the epoch.  When the last chunk of every stream is here, every
+    // workgroup of this launch has read the epoch (each holds at least one
+    // item): advance it for the next launch.
+    if (multi && last && tid == 0) {
+      const unsigned d = __hip_atomic_fetch_add(a.hdr + HDR_DONE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (d == (unsigned)a.nstream - 1u) {
+        __hip_atomic_store(a.hdr + HDR_DONE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.hdr + HDR_EPOCH, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+
+    // Re-run the lane's rows from its true start state and store y.
+    float ew[VW];  // state before this wavefront's first row, zero carry into the chunk
+#pragma unroll
+    for (int j = 0; j < VW; ++j) ew[j] = 0.0f;
+    for (int w = 0; w < wave; ++w) {
+#pragma unroll
+      for (int j = 0; j < VW; ++j) ew[j] = mW * ew[j] + sm.wt[w][ds * VW + j];
+    }
+    const float mg = sm.pw[g];
+    const float mgw = sm.pw[gw];
     float st[VW];
 #pragma unroll
-    for (int j = 0; j < VW; ++j) st[j] = mg * s_carry[ds * VW + j] + (mgw * ew[j] + xin[j]);
+    for (int j = 0; j < VW; ++j) st[j] = mg * sm.carry[ds * VW + j] + (mgw * ew[j] + acc[j]);
     TO* op = static_cast<TO*>(a.out) + b * a.ob + h * a.oh + (int64_t)ds * VW + rbase * a.on;
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       if (rbase + i < a.N) {
         float v[VW], y[VW];
+        opaque(raw[i]);
         unpack16<TI>(raw[i], v);
-        const float rz = s_rz[g * R + i];
+        const float rz = sm.rz[g * R + i];
 #pragma unroll
         for (int j = 0; j < VW; ++j) {
           st[j] = lam * st[j] + v[j];
@@ -400,22 +435,29 @@ __global__ __launch_bounds__(NW * 64) void scan_chunked(ScanArgs a) {
         }
       }
     }
-  } else if (tid == 0) {
-    __hip_atomic_store(a.hdr + HDR_ERROR, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+};
 
-  // 8. The last workgroup to finish rewinds the ticket and advances the epoch.
-  // Every workgroup's ticket RMW has returned before its done RMW is issued,
-  // and RMWs are performed at the device coherence point, so when done reaches
-  // total every ticket has been drawn.
-  if (multi && tid == 0) {
-    const unsigned d = __hip_atomic_fetch_add(a.hdr + HDR_DONE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (d == total - 1u) {
-      __hip_atomic_store(a.hdr + HDR_TICKET, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(a.hdr + HDR_DONE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(a.hdr + HDR_EPOCH, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
+// The launch epoch, read by every thread before it loads any rows (so that
+// waiting for it does not wait for them).
+__device__ __forceinline__ unsigned read_epoch(const ScanArgs& a) {
+  if (a.nchunk <= 1) return 0u;
+  return __hip_atomic_load(a.hdr + HDR_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One item per workgroup: workgroup b owns item b.  An item only waits on
+// items with smaller indices, which are dispatched first (workgroups are
+// dispatched in index order on each XCD), so the smallest unfinished item
+// can always run: no co-residency requirement and no ticket counter.
+template <typename TI, typename TO, int LPR, int R, int NW, int W, int WPE>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, 8)))
+void scan_chunked(ScanArgs a) {
+  using CS = ChunkScan<TI, TO, LPR, R, NW, W>;
+  __shared__ typename CS::Smem sm;
+  const unsigned epoch = read_epoch(a);
+  uint4 raw[R];
+  const float lam = CS::load(a, blockIdx.x, raw);
+  CS::process(a, blockIdx.x, raw, lam, epoch, sm);
 }
 
 // --------------------------------------------------------------------------
@@ -509,10 +551,14 @@ int elem_size(int dt) { return dt == KDECAY_F32 ? 4 : 2; }
 bool dtype_ok(int dt) { return dt == KDECAY_F32 || dt == KDECAY_BF16 || dt == KDECAY_F16; }
 
 // Launch shape of the chunked scan: a chunk holds NW * 64 lanes x R rows x
-// 16 bytes = 32 KiB of input whatever the dtype and D.
-constexpr int kR = 8;
+// 16 bytes = 64 KiB of input whatever the dtype and D, in 64 VGPRs per lane;
+// two wavefronts per SIMD (2 workgroups per CU) leave every lane 256 VGPRs.
+// Measured on MI355X at B=8 N=4096 H=12 D=64 bf16 against R in {8..32},
+// NW in {2,4,8}, W in {2,4,8}: this is the fastest.
+constexpr int kR = 16;
 constexpr int kNW = 4;
-constexpr int kW = 16;
+constexpr int kW = 4;
+constexpr int kWPE = 2;
 
 int64_t chunk_rows(int v_dtype, int64_t D) {
   const int64_t vw = 16 / elem_size(v_dtype);
@@ -527,11 +573,11 @@ bool head_dim_ok(int v_dtype, int64_t D) {
   return lpr >= 1 && lpr <= 64;
 }
 
-template <typename TI, typename TO, int D>
+template <typename TI, typename TO, int D, int R = kR, int NW = kNW, int W = kW, int WPE = kWPE>
 int launch_chunked(const ScanArgs& a, int64_t grid, hipStream_t s) {
   constexpr int VW = 16 / (int)sizeof(TI);
   constexpr int LPR = D / VW;
-  hipLaunchKernelGGL((scan_chunked<TI, TO, LPR, kR, kNW, kW>), dim3((unsigned)grid), dim3(kNW * 64), 0, s, a);
+  hipLaunchKernelGGL((scan_chunked<TI, TO, LPR, R, NW, W, WPE>), dim3((unsigned)grid), dim3(NW * 64), 0, s, a);
   return hip_check("scan_chunked launch");
 }
 

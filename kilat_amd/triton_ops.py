@@ -79,16 +79,20 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> Optional[torch
     return ws
 
 
-def workspace_error(V: torch.Tensor) -> int:
-    """Error word of the workspace used for V's device and current stream.
+def workspace_error(V: torch.Tensor, clear: bool = False) -> int:
+    """Sticky error word of the workspace used for V's device and current stream.
 
-    0: no fault.  1: a look-back gave up waiting (the output is wrong).
-    2: a workgroup drew an impossible ticket.  Synchronises the stream.
+    0: no fault.  1: a look-back of some earlier launch gave up waiting (that
+    launch's output is wrong).  clear=True zeroes the whole workspace after
+    reading it (the word stays set until then).  Synchronises the stream.
     """
     ws = _workspaces.get((V.device.index, _stream_ptr(V.device)))
     if ws is None:
         return 0
-    return int(ws[12:16].view(torch.int32).item())
+    err = int(ws[8:12].view(torch.int32).item())
+    if err and clear:
+        ws.zero_()
+    return err
 
 
 def _lam32(lam: torch.Tensor, H: int, device: torch.device) -> torch.Tensor:

@@ -50,11 +50,11 @@ def test_version(kdecay_lib):
 
 def test_workspace_bytes(kdecay_lib):
     ws = kdecay_lib.kdecay_scan_workspace_bytes
-    # bf16 D=64: 256-row chunks; 16 chunks x 96 streams x 64 words + header
-    assert ws(8, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + 8 * 12 * 16 * 64 * 8
-    assert ws(2, 6, 256, 64, _lib.KDECAY_BF16) == 0  # one chunk per stream
-    assert ws(2, 6, 1024, 64, _lib.KDECAY_F32) == 256 + 2 * 6 * 8 * 64 * 8  # 128-row chunks
-    assert ws(1, 16, 65536, 128, _lib.KDECAY_BF16) == 256 + 16 * 512 * 128 * 8
+    # chunks hold 64 KiB of input: bf16 D=64 -> 512 rows; 8 chunks x 96 streams x 64 words + header
+    assert ws(8, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + 8 * 12 * 8 * 64 * 8
+    assert ws(2, 6, 512, 64, _lib.KDECAY_BF16) == 0  # one chunk per stream
+    assert ws(2, 6, 1024, 64, _lib.KDECAY_F32) == 256 + 2 * 6 * 4 * 64 * 8  # 256-row chunks
+    assert ws(1, 16, 65536, 128, _lib.KDECAY_BF16) == 256 + 16 * 256 * 128 * 8
     assert ws(2, 6, 1024, 48, _lib.KDECAY_BF16) == 0  # unsupported D
 
 

@@ -23,8 +23,9 @@ DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
 
 
 def chunk_rows(dtype, D):
+    """Rows per chunk of the library's scan: 256 lanes x 16 rows x 16 bytes."""
     vw = 16 // torch.empty((), dtype=dtype).element_size()
-    return 4 * (64 // (D // vw)) * 8
+    return 4 * (64 // (D // vw)) * 16
 
 
 def gpu_scan(lam, V, dev, **kw):
@@ -172,7 +173,7 @@ def test_chunked_prefill_with_carry(hip_device, kdecay_lib, dname):
 def test_lambda_edges_match_oracle(hip_device, kdecay_lib):
     g = torch.Generator().manual_seed(11)
     lam = torch.tensor([0.0, 1.0, 0.5, 1e-30])
-    V = torch.randn(2, 4, 600, 16, generator=g)
+    V = torch.randn(2, 4, 2500, 16, generator=g)  # 3 chunks of 1024 rows: edges cross the carry
     V[0, 1, 0, :3] = 0.0
     y = gpu_scan(lam, V, hip_device).cpu()
     ref = O.global_decay(lam, V)
