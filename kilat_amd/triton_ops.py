@@ -12,8 +12,8 @@ Python loop, attention.py:383-394), a position offset for chunked prefill and
 an fp32 output for bf16/fp16 input.
 
 Only HIP tensors are accepted.  There is no CPU path here: a CPU tensor, or a
-missing libkdecay.so, raises.  (kilat_amd.integration keeps the reference's
-own CPU function for CPU tensors when it patches kilat.)
+missing libkdecay.so, raises.  (A Kilat model that runs on the CPU is simply
+not patched by kilat_amd.integration and keeps Kilat's own function.)
 """
 from __future__ import annotations
 

@@ -128,3 +128,23 @@ def test_ctypes_signatures_cover_header(kdecay_lib):
     # silently truncate size_t / pointer returns to int)
     for sym in declared_symbols():
         assert getattr(kdecay_lib, sym).restype in (ctypes.c_int, ctypes.c_size_t, ctypes.c_char_p), sym
+
+
+def test_integration_patches_every_module_by_name():
+    import types
+
+    import kilat_amd
+    from kilat_amd import integration
+
+    def ref_op(lam, V):
+        return "reference"
+
+    mods = [types.ModuleType(n) for n in integration.KILAT_MODULES]
+    for m in mods:
+        m.triton_global_decay = ref_op
+    prev = integration.install(mods)
+    assert all(m.triton_global_decay is kilat_amd.triton_global_decay for m in mods)
+    integration.uninstall(prev)
+    assert all(m.triton_global_decay is ref_op for m in mods)
+    with pytest.raises(AttributeError):
+        integration.install([types.ModuleType("kilat.arc.blocks")])
