@@ -50,11 +50,13 @@ def test_version(kdecay_lib):
 
 def test_workspace_bytes(kdecay_lib):
     ws = kdecay_lib.kdecay_scan_workspace_bytes
-    # chunks hold 64 KiB of input: bf16 D=64 -> 512 rows; 8 chunks x 96 streams x 64 words + header
+    # A stream is a (b,h) pair and a 128-byte channel group; a chunk holds 64 KiB of
+    # input: 512 rows of a 128-byte group.  Words: one per channel per chunk.
     assert ws(8, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + 8 * 12 * 8 * 64 * 8
     assert ws(2, 6, 512, 64, _lib.KDECAY_BF16) == 0  # one chunk per stream
-    assert ws(2, 6, 1024, 64, _lib.KDECAY_F32) == 256 + 2 * 6 * 4 * 64 * 8  # 256-row chunks
-    assert ws(1, 16, 65536, 128, _lib.KDECAY_BF16) == 256 + 16 * 256 * 128 * 8
+    assert ws(2, 6, 1024, 64, _lib.KDECAY_F32) == 256 + 2 * 6 * 2 * 64 * 8  # 2 groups of 32
+    assert ws(1, 16, 65536, 128, _lib.KDECAY_BF16) == 256 + 16 * 128 * 128 * 8
+    assert ws(1, 2, 4096, 32, _lib.KDECAY_BF16) == 256 + 2 * 4 * 32 * 8  # 32-channel rows: 1024-row chunks
     assert ws(2, 6, 1024, 48, _lib.KDECAY_BF16) == 0  # unsupported D
 
 

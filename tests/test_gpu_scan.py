@@ -23,9 +23,11 @@ DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
 
 
 def chunk_rows(dtype, D):
-    """Rows per chunk of the library's scan: 256 lanes x 16 rows x 16 bytes."""
-    vw = 16 // torch.empty((), dtype=dtype).element_size()
-    return 4 * (64 // (D // vw)) * 16
+    """Rows per chunk of the library's scan: 256 lanes x 16 rows x 16 bytes of one
+    channel group of at most 128 bytes."""
+    es = torch.empty((), dtype=dtype).element_size()
+    dg = min(D, 128 // es)
+    return 4 * (64 // (dg // (16 // es))) * 16
 
 
 def gpu_scan(lam, V, dev, **kw):
