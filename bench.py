@@ -143,10 +143,36 @@ def bench_decode(torch, kilat_amd, dev, steps=500):
     if rc[0]:
         raise RuntimeError("kdecay_step failed")
     us = region * 1e3 / steps
+    # The same steps replayed from a HIP graph: 128 launches captured once, so
+    # the host launch cost is gone and the per-step figure is the GPU's own.
+    gsteps = 128
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        gargs = list(args)
+        gargs[-1] = side.cuda_stream
+        with torch.cuda.graph(graph, stream=side):
+            for _ in range(gsteps):
+                rc[0] |= lib.kdecay_step(*gargs)
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(5):
+        graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    if rc[0]:
+        raise RuntimeError("kdecay_step failed under capture")
+    us_graph = t0.elapsed_time(t1) * 1e3 / (5 * gsteps)
+    nbytes = S * H * D * (4 + 2 + 4 + 4)
     return {"config": "C3: 256 seqs x 12 heads x 64, bf16 v_t, fp32 state, per-sequence t_pos",
-            "us_per_step": round(us, 3), "kernel_us_events": round(statistics.median(per) * 1e3, 3),
-            "tokens_per_s": round(S / (us * 1e-6), 1),
-            "bytes_per_step": S * H * D * (4 + 2 + 4 + 4)}
+            "us_per_step": round(us, 3), "us_per_step_graph": round(us_graph, 3),
+            "kernel_us_events": round(statistics.median(per) * 1e3, 3),
+            "tokens_per_s": round(S / (us * 1e-6), 1), "tokens_per_s_graph": round(S / (us_graph * 1e-6), 1),
+            "bytes_per_step": nbytes, "GBps_graph": round(nbytes / (us_graph * 1e-6) / 1e9, 1)}
 
 
 def bench_long(torch, kilat_amd, dev, steps=20):

@@ -600,6 +600,58 @@ __global__ __launch_bounds__(256) void decay_step(StepArgs a) {
   static_cast<TO*>(a.out)[idx] = from_f32<TO>(ns / z_of(lam, tp));
 }
 
+// Four consecutive elements of T as floats / from floats (T: float, 16 bytes;
+// bf16 or fp16, 8 bytes).  p must be aligned to the access size.
+template <typename T>
+__device__ __forceinline__ void load4(const T* p, float (&f)[4]) {
+  if constexpr (sizeof(T) == 4) {
+    const float4 x = *reinterpret_cast<const float4*>(p);
+    f[0] = x.x; f[1] = x.y; f[2] = x.z; f[3] = x.w;
+  } else {
+    const uint2 x = *reinterpret_cast<const uint2*>(p);
+    const uint4 u = make_uint4(x.x, x.y, 0u, 0u);
+    float g[8];
+    unpack16<T>(u, g);
+    f[0] = g[0]; f[1] = g[1]; f[2] = g[2]; f[3] = g[3];
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* p, const float (&f)[4]) {
+  if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<float4*>(p) = make_float4(f[0], f[1], f[2], f[3]);
+  } else {
+    *reinterpret_cast<uint2*>(p) = make_uint2(pack2((T*)nullptr, f[0], f[1]), pack2((T*)nullptr, f[2], f[3]));
+  }
+}
+
+// Decode step, four channels per thread (D % 4 == 0, aligned arrays).  The
+// decay factor and the position are loaded first so the normaliser is
+// computed while the state and v_t are in flight; z is evaluated once per
+// thread instead of once per element.
+template <typename TV, typename TO>
+__global__ __launch_bounds__(256) void decay_step4(StepArgs a) {
+  const int64_t idx = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (idx >= a.total) return;
+  const int64_t bh = idx / a.D;
+  const int64_t h = bh % a.H;
+  const int64_t b = bh / a.H;
+  const float lam = a.lam[h];
+  const int64_t tp = a.tpos ? (int64_t)a.tpos[b] : a.tpos_scalar;
+  float s[4], v[4];
+  load4<float>(a.s_in + idx, s);
+  load4<TV>(static_cast<const TV*>(a.v) + idx, v);
+  const float z = z_of(lam, tp);
+  float ns[4], o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    ns[j] = lam * s[j] + v[j];  // two roundings (contraction is off)
+    o[j] = ns[j] / z;
+  }
+  store4<float>(a.s_out + idx, ns);
+  store4<TO>(static_cast<TO*>(a.out) + idx, o);
+}
+
 // Final state of an empty sequence: the initial state (or zeros).
 __global__ __launch_bounds__(256) void copy_state(const float* init, float* fin, int64_t n) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -684,9 +736,18 @@ int launch_seq(const SeqArgs& a, hipStream_t s) {
   return hip_check("scan_sequential launch");
 }
 
+// The four-wide kernel when D is a multiple of 4 and every array is aligned
+// to its 4-element access, else one thread per element.
 template <typename TV, typename TO>
 int launch_step(const StepArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((decay_step<TV, TO>), dim3((unsigned)((a.total + 255) / 256)), dim3(256), 0, s, a);
+  const bool vec = a.D % 4 == 0 && (uintptr_t)a.s_in % 16 == 0 && (uintptr_t)a.s_out % 16 == 0 &&
+                   (uintptr_t)a.v % (4 * sizeof(TV)) == 0 && (uintptr_t)a.out % (4 * sizeof(TO)) == 0;
+  if (vec) {
+    const int64_t nq = a.total / 4;
+    hipLaunchKernelGGL((decay_step4<TV, TO>), dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((decay_step<TV, TO>), dim3((unsigned)((a.total + 255) / 256)), dim3(256), 0, s, a);
+  }
   return hip_check("decay_step launch");
 }
 

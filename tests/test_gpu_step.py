@@ -116,3 +116,67 @@ def test_scan_then_steps_continue_the_sequence(hip_device, kdecay_lib):
     y = torch.stack(outs, 2).cpu()
     assert float(((y - ref[:, :, 500:]).abs().amax() / ref[:, :, 500:].abs().amax())) <= 1e-5
     assert float(((s.cpu() - sref).abs().amax() / sref.abs().amax())) <= 1e-5
+
+
+def test_step_scalar_fallback_layouts(hip_device, kdecay_lib):
+    """Head dims that are not a multiple of 4, and a misaligned state, use the
+    one-element-per-thread kernel; results are the same bits."""
+    g = torch.Generator().manual_seed(23)
+    lam = lam_uniform(3, 0.5, 0.999, g)
+    for D in (6, 13, 64):
+        state = torch.randn(5, 3, D, generator=g) * 3
+        v = torch.randn(5, 3, D, generator=g).to(torch.bfloat16)
+        dev_state = state.to(hip_device)
+        if D == 64:  # state at a 4-byte offset: not 16-byte aligned
+            buf = torch.zeros(state.numel() + 1, device=hip_device)
+            buf[1:].copy_(state.reshape(-1).to(hip_device))
+            dev_state = buf[1:].view(5, 3, D)
+        print(f"  step fallback D={D}", flush=True)
+        out, ns = kilat_amd.decay_step(lam.to(hip_device), dev_state, v.to(hip_device), 11)
+        torch.cuda.synchronize()
+        ro, rs = O.step(lam, state, v, 11)
+        assert torch.equal(ns.cpu(), rs), D
+        assert ulps(out, ro).max() <= 1, D
+
+
+def test_graph_capture_scan_and_step_replays(hip_device, kdecay_lib):
+    """The scan (its workspace advances its own epoch) and the decode step
+    replay correctly from a HIP graph: several replays, eager work between
+    them, every replay checked against the eager result."""
+    g = torch.Generator().manual_seed(24)
+    lam = lam_uniform(4, 0.5, 0.999, g).to(hip_device)
+    V = torch.randn(2, 4, 3000, 64, generator=g).to(torch.bfloat16).to(hip_device)
+    s0 = torch.randn(2, 4, 64, generator=g).to(hip_device)
+    v = torch.randn(2, 4, 64, generator=g).to(torch.bfloat16).to(hip_device)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        # eager warm-up on the capture stream creates the scan's workspace outside the capture
+        y_ref, fin_ref = kilat_amd.global_decay_scan(lam, V, return_final_state=True)
+        o_ref, ns_ref = kilat_amd.decay_step(lam, fin_ref, v, 3000)
+        y = torch.empty_like(y_ref)
+        fin = torch.empty_like(fin_ref)
+        o = torch.empty_like(o_ref)
+        ns = torch.empty_like(ns_ref)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            y2, fin2 = kilat_amd.global_decay_scan(lam, V, return_final_state=True)
+            o2, ns2 = kilat_amd.decay_step(lam, fin2, v, 3000)
+            y.copy_(y2)
+            fin.copy_(fin2)
+            o.copy_(o2)
+            ns.copy_(ns2)
+    torch.cuda.synchronize()
+    for r in range(4):
+        print(f"  graph replay {r}", flush=True)
+        y.zero_(); o.zero_(); ns.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_ref) and torch.equal(fin, fin_ref), r
+        assert torch.equal(o, o_ref) and torch.equal(ns, ns_ref), r
+        # eager launches between replays share the workspace of the capture stream
+        with torch.cuda.stream(stream):
+            ye = kilat_amd.global_decay_scan(lam, V)
+        torch.cuda.synchronize()
+        assert torch.equal(ye, y_ref)
+    assert kilat_amd.workspace_error(V) == 0
