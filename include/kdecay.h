@@ -116,6 +116,65 @@ int kdecay_scan_fwd_sequential(const void* V, int v_dtype,
                                void* stream);
 
 /*
+ * Forward scan for training: kdecay_scan_fwd, plus the states the backward
+ * pass needs (the state at every kdecay_scan_bwd chunk boundary, so the
+ * backward recomputes s inside each chunk without a second look-back).
+ * The reference has no GPU backward (its Triton path returns a tensor with no
+ * autograd graph, triton_ops.py:309-330); its CPU path is differentiated by
+ * torch autograd through /root/reference/src/kilat/arc/triton_ops.py:240-246.
+ * This pair replaces that autograd path on the GPU.
+ *
+ *   states         fp32, kdecay_scan_saved_states_floats() floats (may be NULL
+ *                  when that is 0); pass it unchanged to kdecay_scan_bwd.
+ * Every other argument as kdecay_scan_fwd.
+ */
+int kdecay_scan_fwd_train(const void* V, int v_dtype, const int64_t* v_strides,
+                          void* out, int out_dtype, const int64_t* out_strides,
+                          const float* lam, const float* init_state,
+                          float* final_state, float* states,
+                          size_t states_floats, int64_t B, int64_t H,
+                          int64_t N, int64_t D, int64_t t_offset,
+                          void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/* Floats of the states buffer kdecay_scan_fwd_train fills (0: none needed). */
+size_t kdecay_scan_saved_states_floats(int64_t B, int64_t H, int64_t N,
+                                       int64_t D, int v_dtype);
+
+/*
+ * Backward of the full-sequence scan (see kdecay_scan_fwd_train):
+ *   g_t  = gy_t / z_t + lam * g_{t+1}   (+ g_final at t = N-1; g_N = 0)
+ *   dV   = g,   d_init = lam * g_0,
+ *   dlam[h] = sum over b, d, t of  g_t * s_{t-1} + gy_t * s_t * d(1/z_t)/dlam
+ * with s the forward states (s_{-1} = init_state or 0).
+ *
+ *   V, gy, dV    [B,H,N,D] of v_dtype (gy and dV share V's dtype), strided as
+ *                kdecay_scan_fwd's V
+ *   lam, init_state, t_offset   as given to the forward call
+ *   states       the forward call's states (NULL allowed when
+ *                kdecay_scan_saved_states_floats() is 0)
+ *   g_final      nullable fp32 [B,H,D]: gradient of the forward's final state
+ *   dlam         fp32 [H], overwritten (summed over B, D and t in a fixed
+ *                order: deterministic)
+ *   d_init       nullable fp32 [B,H,D]
+ *   workspace    kdecay_scan_bwd_workspace_bytes() bytes, 256-byte aligned,
+ *                zeroed once; same rules as kdecay_scan_fwd's (it may be the
+ *                same buffer when large enough)
+ */
+int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides,
+                    const void* gy, const int64_t* gy_strides, void* dV,
+                    const int64_t* dv_strides, const float* lam,
+                    const float* init_state, const float* states,
+                    const float* g_final, float* dlam, float* d_init,
+                    int64_t B, int64_t H, int64_t N, int64_t D,
+                    int64_t t_offset, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/* Bytes of workspace kdecay_scan_bwd needs for this shape. */
+size_t kdecay_scan_bwd_workspace_bytes(int64_t B, int64_t H, int64_t N,
+                                       int64_t D, int v_dtype);
+
+/*
  * Incremental (decode) step for a whole batch, one launch.
  * Replaces the inline update
  *   new_state = lam.view(1,H,1) * past_state + V_current

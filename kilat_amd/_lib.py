@@ -29,6 +29,10 @@ KDECAY_EWORKSPACE = -5
 EXPORTS = (
     "kdecay_scan_fwd",
     "kdecay_scan_workspace_bytes",
+    "kdecay_scan_fwd_train",
+    "kdecay_scan_saved_states_floats",
+    "kdecay_scan_bwd",
+    "kdecay_scan_bwd_workspace_bytes",
     "kdecay_scan_fwd_sequential",
     "kdecay_step",
     "kdecay_version",
@@ -65,6 +69,33 @@ def load() -> ctypes.CDLL:
     ]
     lib.kdecay_scan_workspace_bytes.restype = ctypes.c_size_t
     lib.kdecay_scan_workspace_bytes.argtypes = [_c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int]
+    lib.kdecay_scan_fwd_train.restype = ctypes.c_int
+    lib.kdecay_scan_fwd_train.argtypes = [
+        _c_ptr, ctypes.c_int, _c_i64p,      # V, v_dtype, v_strides
+        _c_ptr, ctypes.c_int, _c_i64p,      # out, out_dtype, out_strides
+        _c_ptr, _c_ptr, _c_ptr,             # lam, init_state, final_state
+        _c_ptr, ctypes.c_size_t,            # states, states_floats
+        _c_i64, _c_i64, _c_i64, _c_i64,     # B, H, N, D
+        _c_i64,                             # t_offset
+        _c_ptr, ctypes.c_size_t,            # workspace, workspace_bytes
+        _c_ptr,                             # stream
+    ]
+    lib.kdecay_scan_saved_states_floats.restype = ctypes.c_size_t
+    lib.kdecay_scan_saved_states_floats.argtypes = [_c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int]
+    lib.kdecay_scan_bwd.restype = ctypes.c_int
+    lib.kdecay_scan_bwd.argtypes = [
+        _c_ptr, ctypes.c_int, _c_i64p,      # V, v_dtype, v_strides
+        _c_ptr, _c_i64p,                    # gy, gy_strides
+        _c_ptr, _c_i64p,                    # dV, dv_strides
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr,     # lam, init_state, states, g_final
+        _c_ptr, _c_ptr,                     # dlam, d_init
+        _c_i64, _c_i64, _c_i64, _c_i64,     # B, H, N, D
+        _c_i64,                             # t_offset
+        _c_ptr, ctypes.c_size_t,            # workspace, workspace_bytes
+        _c_ptr,                             # stream
+    ]
+    lib.kdecay_scan_bwd_workspace_bytes.restype = ctypes.c_size_t
+    lib.kdecay_scan_bwd_workspace_bytes.argtypes = [_c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int]
     lib.kdecay_scan_fwd_sequential.restype = ctypes.c_int
     lib.kdecay_scan_fwd_sequential.argtypes = [
         _c_ptr, ctypes.c_int, _c_i64p,

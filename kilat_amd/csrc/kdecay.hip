@@ -315,6 +315,12 @@ struct ScanArgs {
   int nstream;  // B*H*ng
   u64* flags;   // [nstream][nchunk][DG] look-back words (null if nchunk == 1)
   unsigned* hdr;
+  // Optional: the state after every `state_rows` rows, for the backward pass.
+  // states[(stream * nsaved + k) * DG + c] = s at row k * state_rows - 1
+  // (1 <= k < nsaved = ceil(N / state_rows); entry 0 is not written).
+  float* states;
+  int64_t state_rows;
+  int64_t nsaved;
 };
 
 // 16-byte load of data read exactly once (non-temporal: no cache residency).
@@ -513,6 +519,14 @@ struct ChunkScan {
         }
       }
     }
+    if (a.states) {
+      const int64_t e = rbase + R;  // st is the state at row e - 1
+      if (e < a.N && e % a.state_rows == 0) {
+        float* sp = a.states + ((int64_t)stream * a.nsaved + e / a.state_rows) * DG + ds * VW;
+#pragma unroll
+        for (int j = 0; j < VW; ++j) sp[j] = st[j];
+      }
+    }
   }
 };
 
@@ -536,6 +550,352 @@ void scan_chunked(ScanArgs a) {
   uint4 raw[R];
   const float lam = CS::load(a, blockIdx.x, raw);
   CS::process(a, blockIdx.x, raw, lam, epoch, sm);
+}
+
+// --------------------------------------------------------------------------
+// Backward of the full-sequence scan
+// --------------------------------------------------------------------------
+// For y_t = s_t / z_t, s_t = lam * s_{t-1} + v_t and upstream gradient gy:
+//   u_t  = gy_t / z_t  (+ the final-state gradient at t = N-1)
+//   g_t  = u_t + lam * g_{t+1}           (reverse-time decay scan; g_N = 0)
+//   dV_t = g_t,  d(init) = lam * g_0
+//   dlam = sum_t g_t * s_{t-1} + sum_t gy_t * s_t * d(1/z_t)/dlam
+// One workgroup per chunk, chunks taken from the end of the sequence: the
+// reverse scan uses the forward scan's look-back with the chunk order
+// reversed.  s is recomputed inside each chunk from the state the forward
+// pass saved at the chunk's first row (ScanArgs::states), so no second
+// look-back is needed.  Each chunk writes its dlam partial; a second kernel
+// sums them per head in a fixed order (deterministic).
+struct BwdArgs {
+  const void* V;
+  const void* gy;
+  void* dv;
+  const float* lam;
+  const float* init;    // [B*H*D] or null
+  const float* states;  // forward states at chunk starts (ScanArgs::states layout), null if nchunk == 1
+  const float* gfin;    // [B*H*D] or null: gradient of the final state
+  float* dinit;         // [B*H*D] or null
+  float* partial;       // [nchunk * nstream] dlam partial per chunk (item order)
+  int64_t vb, vh, vn, gb, gh, gn, db, dh, dn;
+  int64_t H, N, t_offset, D;
+  int ng, nchunk, nstream;
+  int64_t nsaved;
+  u64* flags;
+  unsigned* hdr;
+};
+
+// d(1/z)/dlam for z = (1 - lam^e) / ((1 - lam) + 1e-6), evaluated in double.
+__device__ __forceinline__ float dinvz_dlam(float lam, int64_t e) {
+  const double l = lam;
+  const double p = ipow_f64(l, e - 1);
+  const double A = 1.0 - p * l;
+  const double Bd = (1.0 - l) + 1e-6;
+  return (float)(((double)e * p * Bd - A) / (A * A));
+}
+
+// Value of `x` held K row groups above (row groups S lanes apart; lanes with
+// gw + K >= GW get an unspecified value).
+template <int K, int GW, int S>
+__device__ __forceinline__ float lane_shl(float x) {
+  if constexpr (S == 1 && GW <= 16) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x100 | K, 0xf, 0xf, false));
+  } else {
+    return __shfl_down(x, K * S, 64);
+  }
+}
+
+// Reverse inclusive scan over the GW row groups: acc(g) = acc(g) + lam^(R*K) * acc(g + K).
+template <int K, int GW, int VW, int S>
+__device__ __forceinline__ void group_scan_rev(float (&acc)[VW], int gw, const float* pw) {
+  if constexpr (K < GW) {
+    const float m = pw[K];
+#pragma unroll
+    for (int j = 0; j < VW; ++j) {
+      const float o = lane_shl<K, GW, S>(acc[j]);
+      if (gw + K < GW) acc[j] = __builtin_fmaf(m, o, acc[j]);
+    }
+    group_scan_rev<2 * K, GW, VW, S>(acc, gw, pw);
+  }
+}
+
+template <typename T, int LPR, int R, int NW, int W>
+struct ChunkBwd {
+  static constexpr int VW = 16 / (int)sizeof(T);
+  static constexpr int DG = LPR * VW;
+  static constexpr int GW = 64 / LPR;
+  static constexpr int G = NW * GW;
+  static constexpr int L = G * R;
+  static constexpr int NT = NW * 64;
+  static constexpr int DQ = (DG + 63) / 64;
+  static_assert(G + 1 <= NT, "power table is filled one entry per thread");
+
+  struct Smem {
+    float rz[L];       // 1 / z of each row
+    float rzp[L];      // d(1/z)/dlam of each row
+    float pw[G + 1];   // lam^(R*k)
+    float wt[NW][DG];  // forward per-wavefront totals
+    float rt[NW][DG];  // reverse per-wavefront totals
+    float carry_s[DG]; // state before the chunk's first row
+    float carry_g[DG]; // g after the chunk's last row
+    float red[NW];     // dlam partial per wavefront
+  };
+
+  __device__ static void run(const BwdArgs& a, unsigned epoch, Smem& sm) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool multi = a.nchunk > 1;
+    const int item = blockIdx.x;
+    const int rc = item / a.nstream, stream = item % a.nstream;  // rc: position from the end
+    const int chunk = a.nchunk - 1 - rc;
+    const int64_t bh = stream / a.ng, grp = stream % a.ng;
+    const int64_t b = bh / a.H, h = bh % a.H;
+    const int64_t c0 = bh * a.D + grp * DG;
+    const int64_t row0 = (int64_t)chunk * L;
+    const int ds = lane % LPR, gw = lane / LPR;
+    const int g = wave * GW + gw;
+    const int64_t rbase = row0 + (int64_t)g * R;
+    const float lam = a.lam[h];
+
+    // Rows of V and gy (rows past the end re-read row N-1; their u is zeroed
+    // below and their states are never used).
+    uint4 rv[R], rg[R];
+    {
+      const T* vp = static_cast<const T*>(a.V) + b * a.vb + h * a.vh + grp * DG + (int64_t)ds * VW;
+      const T* gp = static_cast<const T*>(a.gy) + b * a.gb + h * a.gh + grp * DG + (int64_t)ds * VW;
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        const int64_t r = rbase + i < a.N ? rbase + i : a.N - 1;
+        rv[i] = load16_stream(vp + r * a.vn);
+      }
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        const int64_t r = rbase + i < a.N ? rbase + i : a.N - 1;
+        rg[i] = load16_stream(gp + r * a.gn);
+      }
+    }
+
+    __syncthreads();
+    if (tid <= G) sm.pw[tid] = pow_like_torch(lam, (int64_t)tid * R);
+    for (int r = tid; r < L; r += NT) {
+      if (row0 + r < a.N) {
+        const int64_t t = a.t_offset + row0 + r;
+        sm.rz[r] = 1.0f / z_of(lam, t);
+        sm.rzp[r] = dinvz_dlam(lam, t + 1);
+      }
+    }
+
+    // Lane-local forward total of v (zero carry in).
+    float fa[VW];
+#pragma unroll
+    for (int j = 0; j < VW; ++j) fa[j] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      float v[VW];
+      unpack16<T>(rv[i], v);
+#pragma unroll
+      for (int j = 0; j < VW; ++j) fa[j] = __builtin_fmaf(lam, fa[j], v[j]);
+    }
+    __syncthreads();  // tables
+
+    // u of every row; lane-local reverse total (zero carry from the right).
+    float u[R][VW];
+    float gfin[VW];
+    const bool has_fin = a.gfin != nullptr && rbase <= a.N - 1 && a.N - 1 < rbase + R;
+#pragma unroll
+    for (int j = 0; j < VW; ++j) gfin[j] = has_fin ? a.gfin[c0 + ds * VW + j] : 0.0f;
+    float ra[VW];
+#pragma unroll
+    for (int j = 0; j < VW; ++j) ra[j] = 0.0f;
+#pragma unroll
+    for (int i = R - 1; i >= 0; --i) {
+      float gv[VW];
+      unpack16<T>(rg[i], gv);
+      const bool valid = rbase + i < a.N;
+      const float rz = valid ? sm.rz[g * R + i] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < VW; ++j) {
+        u[i][j] = valid ? gv[j] * rz : 0.0f;
+        if (rbase + i == a.N - 1) u[i][j] += gfin[j];
+        ra[j] = __builtin_fmaf(lam, ra[j], u[i][j]);
+      }
+    }
+
+    // Scans over the row groups of the wavefront, both directions.
+    group_scan<1, GW, VW, LPR>(fa, gw, sm.pw);
+    group_scan_rev<1, GW, VW, LPR>(ra, gw, sm.pw);
+    if (gw == GW - 1) {
+#pragma unroll
+      for (int j = 0; j < VW; ++j) sm.wt[wave][ds * VW + j] = fa[j];
+    }
+    if (gw == 0) {
+#pragma unroll
+      for (int j = 0; j < VW; ++j) sm.rt[wave][ds * VW + j] = ra[j];
+    }
+    float xin[VW], rin[VW];  // forward: state before the lane; reverse: g after the lane (wave-local)
+#pragma unroll
+    for (int j = 0; j < VW; ++j) {
+      const float o = lane_shr<1, GW, LPR>(fa[j]);
+      xin[j] = gw > 0 ? o : 0.0f;
+      const float p = lane_shl<1, GW, LPR>(ra[j]);
+      rin[j] = gw < GW - 1 ? p : 0.0f;
+    }
+    __syncthreads();
+
+    // Carries of the chunk: the forward state from the forward pass, the
+    // reverse one by look-back over the chunks after this one.
+    const float mW = sm.pw[GW];
+    if (wave == 0) {
+      const float mL = sm.pw[G];
+      const unsigned tag_agg = tag_of(epoch, 0u), tag_inc = tag_of(epoch, 1u);
+      u64* base = multi ? a.flags + (int64_t)stream * a.nchunk * DG : nullptr;
+      float agg[DQ], cg[DQ];
+#pragma unroll
+      for (int q = 0; q < DQ; ++q) {
+        const int d = lane + 64 * q;
+        agg[q] = 0.0f;
+        cg[q] = 0.0f;
+        if (d < DG) {
+#pragma unroll
+          for (int w = NW - 1; w >= 0; --w) agg[q] = __builtin_fmaf(mW, agg[q], sm.rt[w][d]);
+          if (rc > 0 && chunk > 0) publish(base + (int64_t)rc * DG + d, tag_agg, agg[q]);
+          float cs = 0.0f;
+          if (chunk == 0) {
+            if (a.init) cs = a.init[c0 + d];
+          } else {
+            cs = a.states[((int64_t)stream * a.nsaved + chunk) * DG + d];
+          }
+          sm.carry_s[d] = cs;
+        }
+      }
+      if (rc > 0) look_back<W, DG, DQ>(base, rc, tag_agg, tag_inc, mL, a.hdr, cg);
+#pragma unroll
+      for (int q = 0; q < DQ; ++q) {
+        const int d = lane + 64 * q;
+        if (d < DG) {
+          if (multi && chunk > 0) publish(base + (int64_t)rc * DG + d, tag_inc, __builtin_fmaf(mL, cg[q], agg[q]));
+          sm.carry_g[d] = cg[q];
+        }
+      }
+    }
+    __syncthreads();
+
+    // Chunk 0 is the last of its stream in this order; see ChunkScan.
+    if (multi && chunk == 0 && tid == 0) {
+      const unsigned d = __hip_atomic_fetch_add(a.hdr + HDR_DONE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (d == (unsigned)a.nstream - 1u) {
+        __hip_atomic_store(a.hdr + HDR_DONE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.hdr + HDR_EPOCH, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+
+    // The lane's true boundary values.
+    float st[VW], gn[VW];
+    {
+      float ew[VW], er[VW];
+#pragma unroll
+      for (int j = 0; j < VW; ++j) {
+        ew[j] = 0.0f;
+        er[j] = 0.0f;
+      }
+      for (int w = 0; w < wave; ++w) {
+#pragma unroll
+        for (int j = 0; j < VW; ++j) ew[j] = __builtin_fmaf(mW, ew[j], sm.wt[w][ds * VW + j]);
+      }
+      for (int w = NW - 1; w > wave; --w) {
+#pragma unroll
+        for (int j = 0; j < VW; ++j) er[j] = __builtin_fmaf(mW, er[j], sm.rt[w][ds * VW + j]);
+      }
+      const float mg = sm.pw[g], mgw = sm.pw[gw];
+      const float mr = sm.pw[G - 1 - g], mrw = sm.pw[GW - 1 - gw];
+#pragma unroll
+      for (int j = 0; j < VW; ++j) {
+        st[j] = __builtin_fmaf(mg, sm.carry_s[ds * VW + j], __builtin_fmaf(mgw, ew[j], xin[j]));
+        gn[j] = __builtin_fmaf(mr, sm.carry_g[ds * VW + j], __builtin_fmaf(mrw, er[j], rin[j]));
+      }
+    }
+
+    // Reverse pass: g of every row, dV.
+    float gi[R][VW];
+    T* dp = static_cast<T*>(a.dv) + b * a.db + h * a.dh + grp * DG + (int64_t)ds * VW + rbase * a.dn;
+#pragma unroll
+    for (int i = R - 1; i >= 0; --i) {
+#pragma unroll
+      for (int j = 0; j < VW; ++j) {
+        gn[j] = __builtin_fmaf(lam, gn[j], u[i][j]);
+        gi[i][j] = gn[j];
+      }
+      if (rbase + i < a.N) store_vec<T, VW>(dp + (int64_t)i * a.dn, gi[i]);
+    }
+    if (a.dinit && rbase == 0) {
+#pragma unroll
+      for (int j = 0; j < VW; ++j) a.dinit[c0 + ds * VW + j] = lam * gi[0][j];
+    }
+
+    // Forward pass: dlam terms.
+    float dl = 0.0f;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      float v[VW], gv[VW];
+      opaque(rv[i]);
+      opaque(rg[i]);
+      unpack16<T>(rv[i], v);
+      unpack16<T>(rg[i], gv);
+      if (rbase + i < a.N) {
+        const float rzp = sm.rzp[g * R + i];
+#pragma unroll
+        for (int j = 0; j < VW; ++j) {
+          const float s_new = __builtin_fmaf(lam, st[j], v[j]);
+          dl = __builtin_fmaf(gi[i][j], st[j], dl);
+          dl = __builtin_fmaf(gv[j] * rzp, s_new, dl);
+          st[j] = s_new;
+        }
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) dl += __shfl_xor(dl, off, 64);
+    if (lane == 0) sm.red[wave] = dl;
+    __syncthreads();
+    if (tid == 0) {
+      float sum = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) sum += sm.red[w];
+      a.partial[item] = sum;
+    }
+  }
+};
+
+__device__ __forceinline__ unsigned read_epoch_bwd(const BwdArgs& a) {
+  if (a.nchunk <= 1) return 0u;
+  return __hip_atomic_load(a.hdr + HDR_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T, int LPR, int R, int NW, int W>
+__global__ __launch_bounds__(NW * 64) void scan_bwd(BwdArgs a) {
+  using CB = ChunkBwd<T, LPR, R, NW, W>;
+  __shared__ typename CB::Smem sm;
+  const unsigned epoch = read_epoch_bwd(a);
+  CB::run(a, epoch, sm);
+}
+
+// dlam[h] = sum of the chunk partials of head h, in a fixed order, in double.
+__global__ __launch_bounds__(256) void reduce_dlam(const float* partial, float* dlam, int64_t B, int64_t H,
+                                                   int ng, int nchunk, int nstream) {
+  __shared__ double red[256];
+  const int64_t h = blockIdx.x;
+  const int64_t n = B * ng * (int64_t)nchunk;
+  double acc = 0.0;
+  for (int64_t idx = threadIdx.x; idx < n; idx += 256) {
+    const int64_t rc = idx % nchunk, bg = idx / nchunk;
+    const int64_t b = bg / ng, grp = bg % ng;
+    const int64_t stream = (b * H + h) * ng + grp;
+    acc += (double)partial[rc * nstream + stream];
+  }
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  for (int s = 128; s >= 1; s >>= 1) {
+    if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) dlam[h] = (float)red[0];
 }
 
 // --------------------------------------------------------------------------
@@ -652,6 +1012,11 @@ __global__ __launch_bounds__(256) void decay_step4(StepArgs a) {
   store4<TO>(static_cast<TO*>(a.out) + idx, o);
 }
 
+__global__ __launch_bounds__(256) void zero_floats(float* p, int64_t n) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx < n) p[idx] = 0.0f;
+}
+
 // Final state of an empty sequence: the initial state (or zeros).
 __global__ __launch_bounds__(256) void copy_state(const float* init, float* fin, int64_t n) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -729,6 +1094,38 @@ int dispatch_dg(const ScanArgs& a, int64_t DG, int64_t grid, hipStream_t s) {
   return fail(KDECAY_ESHAPE, "unsupported channel group %lld", (long long)DG);
 }
 
+// Launch shape of the backward scan: 4 rows per lane (it holds V, gy and g
+// of its rows in registers), 4 wavefronts.
+constexpr int kRB = 4;
+constexpr int kNWB = 4;
+constexpr int kWB = 4;
+
+int64_t bwd_chunk_rows(int v_dtype, int64_t D) {
+  const int64_t vw = 16 / elem_size(v_dtype);
+  const int64_t lpr = group_width(v_dtype, D) / vw;
+  return kNWB * (64 / lpr) * kRB;
+}
+
+template <typename T, int DG>
+int launch_bwd(const BwdArgs& a, int64_t grid, hipStream_t s) {
+  constexpr int VW = 16 / (int)sizeof(T);
+  constexpr int LPR = DG / VW;
+  hipLaunchKernelGGL((scan_bwd<T, LPR, kRB, kNWB, kWB>), dim3((unsigned)grid), dim3(kNWB * 64), 0, s, a);
+  return hip_check("scan_bwd launch");
+}
+
+template <typename T>
+int dispatch_bwd(const BwdArgs& a, int64_t DG, int64_t grid, hipStream_t s) {
+  switch (DG) {
+    case 16: return launch_bwd<T, 16>(a, grid, s);
+    case 32: return launch_bwd<T, 32>(a, grid, s);
+    case 64:
+      if constexpr (sizeof(T) == 2) return launch_bwd<T, 64>(a, grid, s);
+      break;
+  }
+  return fail(KDECAY_ESHAPE, "unsupported channel group %lld", (long long)DG);
+}
+
 template <typename TI, typename TO>
 int launch_seq(const SeqArgs& a, hipStream_t s) {
   const int64_t n = a.B * a.H * a.D;
@@ -789,10 +1186,10 @@ size_t kdecay_scan_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D, i
   return kHeaderBytes + (size_t)(B * H * nchunk * D) * sizeof(u64);
 }
 
-int kdecay_scan_fwd(const void* V, int v_dtype, const int64_t* v_strides, void* out, int out_dtype,
-                    const int64_t* out_strides, const float* lam, const float* init_state,
-                    float* final_state, int64_t B, int64_t H, int64_t N, int64_t D, int64_t t_offset,
-                    void* workspace, size_t workspace_bytes, void* stream) {
+static int scan_fwd_impl(const void* V, int v_dtype, const int64_t* v_strides, void* out, int out_dtype,
+                         const int64_t* out_strides, const float* lam, const float* init_state,
+                         float* final_state, int64_t B, int64_t H, int64_t N, int64_t D, int64_t t_offset,
+                         void* workspace, size_t workspace_bytes, float* states, void* stream) {
   int rc = check_scan_args(V, v_dtype, v_strides, out, out_dtype, out_strides, lam, B, H, N, D);
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -844,6 +1241,9 @@ int kdecay_scan_fwd(const void* V, int v_dtype, const int64_t* v_strides, void* 
   a.nstream = (int)nstream;
   a.hdr = need ? static_cast<unsigned*>(workspace) : nullptr;
   a.flags = need ? reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes) : nullptr;
+  a.state_rows = bwd_chunk_rows(v_dtype, D);
+  a.nsaved = (N + a.state_rows - 1) / a.state_rows;
+  a.states = a.nsaved > 1 ? states : nullptr;
 
   if (v_dtype == KDECAY_F32) return dispatch_dg<float, float>(a, DG, grid, s);
   if (v_dtype == KDECAY_BF16) {
@@ -852,6 +1252,130 @@ int kdecay_scan_fwd(const void* V, int v_dtype, const int64_t* v_strides, void* 
   }
   if (out_dtype == KDECAY_F16) return dispatch_dg<_Float16, _Float16>(a, DG, grid, s);
   return dispatch_dg<_Float16, float>(a, DG, grid, s);
+}
+
+int kdecay_scan_fwd(const void* V, int v_dtype, const int64_t* v_strides, void* out, int out_dtype,
+                    const int64_t* out_strides, const float* lam, const float* init_state,
+                    float* final_state, int64_t B, int64_t H, int64_t N, int64_t D, int64_t t_offset,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  return scan_fwd_impl(V, v_dtype, v_strides, out, out_dtype, out_strides, lam, init_state, final_state, B, H, N, D,
+                       t_offset, workspace, workspace_bytes, nullptr, stream);
+}
+
+size_t kdecay_scan_saved_states_floats(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
+  if (B <= 0 || H <= 0 || N <= 0 || !dtype_ok(v_dtype) || !head_dim_ok(v_dtype, D)) return 0;
+  const int64_t Lb = bwd_chunk_rows(v_dtype, D);
+  const int64_t nsaved = (N + Lb - 1) / Lb;
+  if (nsaved <= 1) return 0;
+  return (size_t)(B * H * D * nsaved);
+}
+
+int kdecay_scan_fwd_train(const void* V, int v_dtype, const int64_t* v_strides, void* out, int out_dtype,
+                          const int64_t* out_strides, const float* lam, const float* init_state,
+                          float* final_state, float* states, size_t states_floats, int64_t B, int64_t H,
+                          int64_t N, int64_t D, int64_t t_offset, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  const size_t need = kdecay_scan_saved_states_floats(B, H, N, D, v_dtype);
+  if (need && (!states || states_floats < need))
+    return fail(KDECAY_EINVAL, "states buffer of %zu floats required, %zu given", need, states_floats);
+  return scan_fwd_impl(V, v_dtype, v_strides, out, out_dtype, out_strides, lam, init_state, final_state, B, H, N, D,
+                       t_offset, workspace, workspace_bytes, states, stream);
+}
+
+size_t kdecay_scan_bwd_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
+  if (B <= 0 || H <= 0 || N <= 0 || !dtype_ok(v_dtype) || !head_dim_ok(v_dtype, D)) return 0;
+  const int64_t Lb = bwd_chunk_rows(v_dtype, D);
+  const int64_t nchunk = (N + Lb - 1) / Lb;
+  const size_t flags = nchunk > 1 ? (size_t)(B * H * nchunk * D) * sizeof(u64) : 0;
+  const int64_t nstream = B * H * (D / group_width(v_dtype, D));
+  const size_t partial = ((size_t)(nstream * nchunk) * sizeof(float) + 255) & ~(size_t)255;
+  return kHeaderBytes + flags + partial;
+}
+
+int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides, const void* gy,
+                    const int64_t* gy_strides, void* dV, const int64_t* dv_strides, const float* lam,
+                    const float* init_state, const float* states, const float* g_final, float* dlam,
+                    float* d_init, int64_t B, int64_t H, int64_t N, int64_t D, int64_t t_offset,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  if (B < 0 || H < 0 || N < 0 || D < 0) return fail(KDECAY_EINVAL, "negative size");
+  if (!dtype_ok(v_dtype)) return fail(KDECAY_EDTYPE, "unknown dtype code %d", v_dtype);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (B * H * D == 0) return 0;
+  if (!lam || !dlam) return fail(KDECAY_EINVAL, "null pointer argument");
+  if (N == 0) {  // no rows: the gradients are the final-state gradient passed through
+    hipLaunchKernelGGL(copy_state, dim3((unsigned)((B * H * D + 255) / 256)), dim3(256), 0, s, g_final,
+                       d_init, d_init ? B * H * D : 0);
+    int e = hip_check("copy_state launch");
+    if (e) return e;
+    hipLaunchKernelGGL(zero_floats, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, s, dlam, H);
+    return hip_check("zero_floats launch");
+  }
+  if (!V || !gy || !dV || !v_strides || !gy_strides || !dv_strides) return fail(KDECAY_EINVAL, "null pointer argument");
+  if (!head_dim_ok(v_dtype, D))
+    return fail(KDECAY_ESHAPE, "head dim D=%lld not in {16,32,64,128,256}", (long long)D);
+  const int64_t vw = 16 / elem_size(v_dtype);
+  if (v_strides[3] != 1 || gy_strides[3] != 1 || dv_strides[3] != 1)
+    return fail(KDECAY_ELAYOUT, "channel (d) stride must be 1");
+  if (((uintptr_t)V & 15u) || ((uintptr_t)gy & 15u) || ((uintptr_t)dV & 15u))
+    return fail(KDECAY_ELAYOUT, "V, gy and dV must be 16-byte aligned");
+  const int64_t sizes[3] = {B, H, N};
+  for (int k = 0; k < 3; ++k) {
+    if (sizes[k] > 1 && (v_strides[k] % vw || gy_strides[k] % vw || dv_strides[k] % vw))
+      return fail(KDECAY_ELAYOUT, "stride %d is not a multiple of 16 bytes", k);
+  }
+  const int64_t Lb = bwd_chunk_rows(v_dtype, D);
+  const int64_t nchunk = (N + Lb - 1) / Lb;
+  const int64_t DG = group_width(v_dtype, D);
+  const int64_t nstream = B * H * (D / DG);
+  const int64_t grid = nchunk * nstream;
+  if (grid > 0x7fffffffLL) return fail(KDECAY_EINVAL, "problem too large (%lld chunks)", (long long)grid);
+  if (nchunk > 1 && !states) return fail(KDECAY_EINVAL, "saved states (kdecay_scan_fwd_train) required");
+  const size_t need = kdecay_scan_bwd_workspace_bytes(B, H, N, D, v_dtype);
+  if (!workspace || workspace_bytes < need)
+    return fail(KDECAY_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+  if ((uintptr_t)workspace & 255u) return fail(KDECAY_EWORKSPACE, "workspace must be 256-byte aligned");
+
+  BwdArgs a;
+  a.V = V;
+  a.gy = gy;
+  a.dv = dV;
+  a.lam = lam;
+  a.init = init_state;
+  a.states = states;
+  a.gfin = g_final;
+  a.dinit = d_init;
+  a.vb = v_strides[0];
+  a.vh = v_strides[1];
+  a.vn = v_strides[2];
+  a.gb = gy_strides[0];
+  a.gh = gy_strides[1];
+  a.gn = gy_strides[2];
+  a.db = dv_strides[0];
+  a.dh = dv_strides[1];
+  a.dn = dv_strides[2];
+  a.H = H;
+  a.N = N;
+  a.t_offset = t_offset;
+  a.D = D;
+  a.ng = (int)(D / DG);
+  a.nchunk = (int)nchunk;
+  a.nstream = (int)nstream;
+  a.nsaved = nchunk;
+  a.hdr = static_cast<unsigned*>(workspace);
+  const size_t flag_bytes = nchunk > 1 ? (size_t)(B * H * nchunk * D) * sizeof(u64) : 0;
+  a.flags = nchunk > 1 ? reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes) : nullptr;
+  a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + kHeaderBytes + flag_bytes);
+  int e;
+  if (v_dtype == KDECAY_F32)
+    e = dispatch_bwd<float>(a, DG, grid, s);
+  else if (v_dtype == KDECAY_BF16)
+    e = dispatch_bwd<__bf16>(a, DG, grid, s);
+  else
+    e = dispatch_bwd<_Float16>(a, DG, grid, s);
+  if (e) return e;
+  hipLaunchKernelGGL(reduce_dlam, dim3((unsigned)H), dim3(256), 0, s, a.partial, dlam, B, H, a.ng, a.nchunk,
+                     a.nstream);
+  return hip_check("reduce_dlam launch");
 }
 
 int kdecay_scan_fwd_sequential(const void* V, int v_dtype, const int64_t* v_strides, void* out,

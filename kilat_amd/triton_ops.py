@@ -102,6 +102,87 @@ def _lam32(lam: torch.Tensor, H: int, device: torch.device) -> torch.Tensor:
     return lam.detach().reshape(H).to(device=device, dtype=torch.float32).contiguous()
 
 
+class _ScanFn(torch.autograd.Function):
+    """The chunked scan with a backward (kdecay_scan_fwd_train / kdecay_scan_bwd).
+
+    Inputs: lam (fp32 [H], differentiable), V, init (fp32 [B,H,D] or None),
+    t_offset, out dtype.  Outputs: (y, final state).  The reference's GPU path
+    has no backward; its CPU path is differentiated by torch autograd through
+    triton_ops.py:240-246, which this replaces on HIP tensors.
+    """
+
+    @staticmethod
+    def forward(ctx, lam32, V, init32, t_offset, out_dtype):
+        B, H, N, D = V.shape
+        dev = V.device
+        v_code = _DTYPE_CODE[V.dtype]
+        o_code = _DTYPE_CODE[out_dtype]
+        Vk = V if _vector_layout_ok(V) else V.contiguous()
+        out = torch.empty(Vk.shape, dtype=out_dtype, device=dev) if out_dtype != Vk.dtype else torch.empty_like(Vk)
+        if not _vector_layout_ok(out):
+            out = torch.empty(Vk.shape, dtype=out_dtype, device=dev)
+        final = torch.empty((B, H, D), dtype=torch.float32, device=dev)
+        lib = _lib.load()
+        nst = lib.kdecay_scan_saved_states_floats(B, H, N, D, v_code)
+        states = torch.empty(max(nst, 1), dtype=torch.float32, device=dev)
+        with torch.cuda.device(dev):
+            stream = _stream_ptr(dev)
+            nbytes = max(lib.kdecay_scan_workspace_bytes(B, H, N, D, v_code),
+                         lib.kdecay_scan_bwd_workspace_bytes(B, H, N, D, v_code))
+            ws = _workspace(dev, stream, nbytes)
+            rc = lib.kdecay_scan_fwd_train(
+                Vk.data_ptr(), v_code, _lib.strides4(Vk.stride()),
+                out.data_ptr(), o_code, _lib.strides4(out.stride()),
+                lam32.data_ptr(), init32.data_ptr() if init32 is not None else None, final.data_ptr(),
+                states.data_ptr(), states.numel(), B, H, N, D, int(t_offset),
+                ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, stream,
+            )
+        _lib.check(rc, "kdecay_scan_fwd_train")
+        ctx.t_offset = int(t_offset)
+        ctx.has_init = init32 is not None
+        ctx.save_for_backward(lam32, Vk, init32 if init32 is not None else final.new_empty(0), states)
+        return out, final
+
+    @staticmethod
+    def backward(ctx, gy, gfin):
+        lam32, Vk, init32, states = ctx.saved_tensors
+        B, H, N, D = Vk.shape
+        dev = Vk.device
+        v_code = _DTYPE_CODE[Vk.dtype]
+        if gy is None:
+            gy = torch.zeros_like(Vk)
+        gy = gy.to(Vk.dtype)
+        if not _vector_layout_ok(gy):
+            gy = gy.contiguous()
+        dV = torch.empty_like(Vk)
+        if not _vector_layout_ok(dV):
+            dV = torch.empty(Vk.shape, dtype=Vk.dtype, device=dev)
+        dlam = torch.empty(H, dtype=torch.float32, device=dev)
+        dinit = torch.empty((B, H, D), dtype=torch.float32, device=dev) if ctx.has_init else None
+        g_fin = gfin.to(torch.float32).contiguous() if gfin is not None else None
+        lib = _lib.load()
+        with torch.cuda.device(dev):
+            stream = _stream_ptr(dev)
+            nbytes = lib.kdecay_scan_bwd_workspace_bytes(B, H, N, D, v_code)
+            ws = _workspace(dev, stream, nbytes)
+            rc = lib.kdecay_scan_bwd(
+                Vk.data_ptr(), v_code, _lib.strides4(Vk.stride()),
+                gy.data_ptr(), _lib.strides4(gy.stride()),
+                dV.data_ptr(), _lib.strides4(dV.stride()),
+                lam32.data_ptr(), init32.data_ptr() if ctx.has_init else None, states.data_ptr(),
+                g_fin.data_ptr() if g_fin is not None else None,
+                dlam.data_ptr(), dinit.data_ptr() if dinit is not None else None,
+                B, H, N, D, ctx.t_offset,
+                ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, stream,
+            )
+        _lib.check(rc, "kdecay_scan_bwd")
+        return dlam, dV, dinit, None, None
+
+
+def _needs_grad(*ts) -> bool:
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
+
+
 def global_decay_scan(
     lam: torch.Tensor,
     V: torch.Tensor,
@@ -128,6 +209,8 @@ def global_decay_scan(
     v_code = _dtype_code(V, "V")
     B, H, N, D = V.shape
     dev = V.device
+    if _needs_grad(lam, V, initial_state):
+        return _scan_with_grad(lam, V, initial_state, return_final_state, t_offset, out, out_dtype, algorithm)
     lam32 = _lam32(lam, H, dev)
     if out is None:
         out = torch.empty_like(V, dtype=out_dtype or V.dtype)
@@ -180,6 +263,34 @@ def global_decay_scan(
     return out
 
 
+def _scan_with_grad(lam, V, initial_state, return_final_state, t_offset, out, out_dtype, algorithm):
+    """global_decay_scan when a gradient is required: the chunked scan under _ScanFn."""
+    B, H, N, D = V.shape
+    dev = V.device
+    if algorithm != "chunked" or D not in VECTOR_HEAD_DIMS or out is not None:
+        raise NotImplementedError(
+            "kilat_amd: gradients need the chunked scan (algorithm='chunked', D in "
+            f"{VECTOR_HEAD_DIMS}, no out=); got algorithm={algorithm!r}, D={D}, out given={out is not None}"
+        )
+    _require_hip(lam, "lam_scores")
+    if lam.numel() != H:
+        raise ValueError(f"kilat_amd: lam_scores has {lam.numel()} elements, V has {H} heads")
+    lam32 = lam.reshape(H).to(device=dev, dtype=torch.float32).contiguous()
+    init32 = None
+    if initial_state is not None:
+        _require_hip(initial_state, "initial_state")
+        if tuple(initial_state.shape) != (B, H, D):
+            raise ValueError(f"kilat_amd: initial_state must be [B,H,D]={B, H, D}")
+        init32 = initial_state.to(device=dev, dtype=torch.float32).contiguous()
+    o_dtype = out_dtype or V.dtype
+    if o_dtype not in (V.dtype, torch.float32):
+        raise TypeError("kilat_amd: out dtype must be V's dtype or float32")
+    y, final = _ScanFn.apply(lam32, V, init32, int(t_offset), o_dtype)
+    if return_final_state:
+        return y, final
+    return y
+
+
 def triton_global_decay(lam_scores: torch.Tensor, V: torch.Tensor) -> torch.Tensor:
     """Drop-in for kilat.arc.triton_ops.triton_global_decay (triton_ops.py:249-330).
 
@@ -187,7 +298,9 @@ def triton_global_decay(lam_scores: torch.Tensor, V: torch.Tensor) -> torch.Tens
     V: [B,H,N,D] on a HIP device.  Returns out = empty_like(V) filled with
     out[:,:,t] = (sum_{j<=t} lam^(t-j) V[:,:,j]) / z_t, z_t as the reference's
     CPU path computes it (triton_ops.py:245).  Enqueued on the current stream,
-    no host synchronisation, no autograd graph (as the reference's GPU path).
+    no host synchronisation.  When lam_scores or V requires grad, the result
+    carries a backward (dV and dlam on the GPU), as the reference's CPU path
+    does through torch autograd; its GPU path has none.
     """
     return global_decay_scan(lam_scores, V)
 

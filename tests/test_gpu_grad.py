@@ -1,0 +1,131 @@
+"""GPU backward of the full-sequence scan (kdecay_scan_fwd_train + kdecay_scan_bwd
+through kilat_amd's autograd Function) against fp64 torch autograd through the
+oracle, which restates /root/reference/src/kilat/arc/triton_ops.py:240-246 (the
+reference's differentiable CPU path; its GPU path has no backward).
+
+Tolerances: dV as the forward (fp32: rel_err <= 1e-5; bf16/fp16: max-abs
+<= 2e-2 relative to the gradient's scale); dlam and d(init) (fp32
+accumulation): relative error <= 1e-4.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import kilat_amd
+from oracle import decay_oracle as O
+from tests.decay_cases import lam_uniform, rel_err
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def oracle_grads(lam, V, gy, init=None, gfin=None, t_offset=0):
+    lam64 = lam.double().requires_grad_(True)
+    V64 = V.double().requires_grad_(True)
+    init64 = init.double().requires_grad_(True) if init is not None else None
+    y, fin = O.scan(lam64, V64, init_state=init64, t_offset=t_offset)
+    loss = (y * gy.double()).sum()
+    if gfin is not None:
+        loss = loss + (fin * gfin.double()).sum()
+    loss.backward()
+    return V64.grad, lam64.grad, (init64.grad if init is not None else None)
+
+
+def gpu_grads(lam, V, gy, dev, init=None, gfin=None, t_offset=0):
+    lam_d = lam.to(dev).requires_grad_(True)
+    V_d = V.to(dev).requires_grad_(True)
+    init_d = init.to(dev).requires_grad_(True) if init is not None else None
+    print(f"  grad V{tuple(V.shape)} {V.dtype} init={init is not None} gfin={gfin is not None}", flush=True)
+    y, fin = kilat_amd.global_decay_scan(lam_d, V_d, initial_state=init_d, return_final_state=True,
+                                         t_offset=t_offset)
+    loss = (y.float() * gy.to(dev).float()).sum()
+    if gfin is not None:
+        loss = loss + (fin * gfin.to(dev)).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    return V_d.grad.cpu(), lam_d.grad.cpu(), (init_d.grad.cpu() if init is not None else None)
+
+
+def rel(a, b):
+    return float((a.double() - b.double()).abs().max() / b.double().abs().max().clamp_min(1e-30))
+
+
+def check(dv, dl, di, rdv, rdl, rdi, dtype, what):
+    if dtype == torch.float32:
+        assert rel_err(dv, rdv) <= 1e-5, f"{what}: dV rel_err {rel_err(dv, rdv):.3e}"
+    else:
+        e = float((dv.double() - rdv).abs().max() / rdv.abs().max())
+        assert e <= 2e-2, f"{what}: dV scaled max-abs {e:.3e}"
+    assert rel(dl, rdl) <= 1e-4, f"{what}: dlam rel {rel(dl, rdl):.3e}"
+    if rdi is not None:
+        assert rel(di, rdi) <= 1e-4, f"{what}: dinit rel {rel(di, rdi):.3e}"
+
+
+@pytest.mark.parametrize("dname", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("D", [16, 64, 128])
+def test_backward_shapes(hip_device, kdecay_lib, dname, D):
+    dtype = DTYPES[dname]
+    g = torch.Generator().manual_seed(200 + D)
+    lam = lam_uniform(3, 0.5, 0.999, g)
+    for N in (1, 77, 300, 1100):
+        V = torch.randn(2, 3, N, D, generator=g).to(dtype)
+        gy = torch.randn(2, 3, N, D, generator=g).to(dtype)
+        dv, dl, _ = gpu_grads(lam, V, gy, hip_device)
+        rdv, rdl, _ = oracle_grads(lam, V, gy)
+        assert dv.dtype == dtype
+        check(dv, dl, None, rdv, rdl, None, dtype, f"D={D} N={N}")
+
+
+def test_backward_init_final_offset(hip_device, kdecay_lib):
+    g = torch.Generator().manual_seed(210)
+    lam = lam_uniform(4, 0.8, 0.9999, g)
+    V = torch.randn(2, 4, 1500, 64, generator=g)
+    gy = torch.randn(2, 4, 1500, 64, generator=g)
+    init = torch.randn(2, 4, 64, generator=g)
+    gfin = torch.randn(2, 4, 64, generator=g)
+    dv, dl, di = gpu_grads(lam, V, gy, hip_device, init=init, gfin=gfin, t_offset=9)
+    rdv, rdl, rdi = oracle_grads(lam, V, gy, init=init, gfin=gfin, t_offset=9)
+    check(dv, dl, di, rdv, rdl, rdi, torch.float32, "init+gfin+offset")
+
+
+def test_backward_c1_shape_and_drop_in(hip_device, kdecay_lib):
+    """C1 (B=2 N=1024 H=6 D=64 fp32) through triton_global_decay, as a training step calls it."""
+    g = torch.Generator().manual_seed(211)
+    log_lambda = torch.log(torch.tensor(0.9 / 0.1)) + 0.5 * torch.randn(6, generator=g)
+    V = torch.randn(2, 6, 1024, 64, generator=g)
+    gy = torch.randn(2, 6, 1024, 64, generator=g)
+    ll = log_lambda.to(hip_device).requires_grad_(True)
+    Vd = V.to(hip_device).requires_grad_(True)
+    y = kilat_amd.triton_global_decay(torch.sigmoid(ll), Vd)
+    (y * gy.to(hip_device)).sum().backward()
+    torch.cuda.synchronize()
+    ll64 = log_lambda.double().requires_grad_(True)
+    V64 = V.double().requires_grad_(True)
+    (O.global_decay(torch.sigmoid(ll64), V64) * gy.double()).sum().backward()
+    assert rel_err(Vd.grad.cpu(), V64.grad) <= 1e-5
+    assert rel(ll.grad.cpu(), ll64.grad) <= 1e-4
+
+
+def test_backward_is_deterministic(hip_device, kdecay_lib):
+    g = torch.Generator().manual_seed(212)
+    lam = lam_uniform(3, 0.5, 0.999, g)
+    V = torch.randn(2, 3, 3000, 64, generator=g).to(torch.bfloat16)
+    gy = torch.randn(2, 3, 3000, 64, generator=g).to(torch.bfloat16)
+    a = gpu_grads(lam, V, gy, hip_device)
+    b = gpu_grads(lam, V, gy, hip_device)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_no_grad_path_unchanged(hip_device, kdecay_lib):
+    """Without requires_grad the inference scan runs (no states are saved)."""
+    g = torch.Generator().manual_seed(213)
+    lam = lam_uniform(2, 0.5, 0.99, g).to(hip_device)
+    V = torch.randn(1, 2, 700, 64, generator=g).to(hip_device)
+    y = kilat_amd.triton_global_decay(lam, V)
+    assert y.grad_fn is None
+    Vg = V.clone().requires_grad_(True)
+    y2 = kilat_amd.triton_global_decay(lam, Vg)
+    torch.cuda.synchronize()
+    assert y2.grad_fn is not None and torch.equal(y, y2.detach())

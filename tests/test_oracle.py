@@ -251,3 +251,56 @@ def test_golden_fixtures_reproduce():
     assert torch.equal(out, t("step_out")) and torch.equal(ns, t("step_new_state"))
     out, ns = O.step(t("step_lam"), t("step_state"), t("step_v", True), [int(x) for x in d["step_tpos"]])
     assert torch.equal(out, t("step_out_vec")) and torch.equal(ns, t("step_new_state_vec"))
+
+
+# --------------------------------------------------------------------------
+# Gradients of the oracle (torch autograd through the restatement of
+# triton_ops.py:240-246) -- the reference for the GPU backward.
+# --------------------------------------------------------------------------
+def _loss(lam, V, gy, init=None, gfin=None, t_offset=0):
+    y, fin = O.scan(lam, V, init_state=init, t_offset=t_offset)
+    total = (y * gy).sum()
+    if gfin is not None:
+        total = total + (fin * gfin).sum()
+    return total
+
+
+def test_oracle_grad_dv_closed_form():
+    """dL/dV_t = sum_{k>=t} lam^(k-t) gy_k / z_k (fp64, brute force)."""
+    g = torch.Generator().manual_seed(30)
+    lam = lam_uniform(3, 0.5, 0.999, g).double()
+    V = torch.randn(2, 3, 23, 4, generator=g, dtype=torch.float64, requires_grad=True)
+    gy = torch.randn(2, 3, 23, 4, generator=g, dtype=torch.float64)
+    _loss(lam, V, gy).backward()
+    l = lam.view(1, 3, 1, 1)
+    t = torch.arange(23, dtype=torch.float64)
+    z = ((1 - l ** (t.view(1, 1, 23, 1) + 1)) / ((1 - l) + 1e-6))
+    u = gy / z
+    ref = torch.zeros_like(u)
+    for ti in range(23):
+        for k in range(ti, 23):
+            ref[:, :, ti] += l[:, :, 0] ** (k - ti) * u[:, :, k]
+    assert torch.allclose(V.grad, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_oracle_grad_dlam_and_init_finite_difference():
+    """Autograd dlam and d(init) against central differences (fp64)."""
+    g = torch.Generator().manual_seed(31)
+    lam = lam_uniform(2, 0.6, 0.99, g).double().requires_grad_(True)
+    V = torch.randn(1, 2, 30, 3, generator=g, dtype=torch.float64)
+    init = torch.randn(1, 2, 3, generator=g, dtype=torch.float64, requires_grad=True)
+    gy = torch.randn(1, 2, 30, 3, generator=g, dtype=torch.float64)
+    gfin = torch.randn(1, 2, 3, generator=g, dtype=torch.float64)
+    _loss(lam, V, gy, init, gfin, t_offset=4).backward()
+    eps = 1e-6
+    for h in range(2):
+        lp, lm = lam.detach().clone(), lam.detach().clone()
+        lp[h] += eps
+        lm[h] -= eps
+        fd = (_loss(lp, V, gy, init.detach(), gfin, 4) - _loss(lm, V, gy, init.detach(), gfin, 4)) / (2 * eps)
+        assert abs(float(fd) - float(lam.grad[h])) <= 1e-6 * max(1.0, abs(float(fd)))
+    ip, im = init.detach().clone(), init.detach().clone()
+    ip[0, 1, 2] += eps
+    im[0, 1, 2] -= eps
+    fd = (_loss(lam.detach(), V, gy, ip, gfin, 4) - _loss(lam.detach(), V, gy, im, gfin, 4)) / (2 * eps)
+    assert abs(float(fd) - float(init.grad[0, 1, 2])) <= 1e-6 * max(1.0, abs(float(fd)))
