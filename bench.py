@@ -213,6 +213,102 @@ def measured_traffic():
         return None
 
 
+def bench_backward(torch, dev, steps=100):
+    """C2-shaped training pass: kdecay_scan_fwd_train, then kdecay_scan_bwd (dV, dlam).
+
+    Algorithmic bytes: forward 4 B/element (V in, y out); backward 6 B/element
+    (V and gy in, dV out).  3 rotated buffer sets (450 MB) keep it out of MALL.
+    """
+    from kilat_amd import _lib
+    from kilat_amd.triton_ops import _stream_ptr, _workspace
+
+    B, H, N, D = 8, 12, 4096, 64
+    lib = _lib.load()
+    code = _lib.KDECAY_BF16
+    g = torch.Generator(device=dev).manual_seed(5)
+    lam = c2_lam(H, torch).to(dev)
+    stream = _stream_ptr(dev)
+    nst = lib.kdecay_scan_saved_states_floats(B, H, N, D, code)
+    nbytes = max(lib.kdecay_scan_workspace_bytes(B, H, N, D, code), lib.kdecay_scan_bwd_workspace_bytes(B, H, N, D, code))
+    ws = _workspace(dev, stream, nbytes)
+    sets = []
+    for _ in range(3):
+        V = torch.randn(B, H, N, D, generator=g, device=dev).to(torch.bfloat16)
+        gy = torch.randn(B, H, N, D, generator=g, device=dev).to(torch.bfloat16)
+        sets.append((V, gy, torch.empty_like(V), torch.empty_like(V), torch.empty(nst, device=dev),
+                     torch.empty(H, device=dev), torch.empty(B, H, D, device=dev)))
+    st = _lib.strides4(sets[0][0].stride())
+    rc = [0]
+
+    def fwd(k):
+        V, gy, y, dV, states, dlam, fin = sets[k % 3]
+        rc[0] |= lib.kdecay_scan_fwd_train(V.data_ptr(), code, st, y.data_ptr(), code, st, lam.data_ptr(), None,
+                                           fin.data_ptr(), states.data_ptr(), nst, B, H, N, D, 0, ws.data_ptr(),
+                                           ws.numel(), stream)
+
+    def bwd(k):
+        V, gy, y, dV, states, dlam, fin = sets[k % 3]
+        rc[0] |= lib.kdecay_scan_bwd(V.data_ptr(), code, st, gy.data_ptr(), st, dV.data_ptr(), st, lam.data_ptr(),
+                                     None, states.data_ptr(), None, dlam.data_ptr(), None, B, H, N, D, 0,
+                                     ws.data_ptr(), ws.numel(), stream)
+
+    rf, _ = time_region(torch, fwd, steps, 10)
+    rb, _ = time_region(torch, bwd, steps, 10)
+    if rc[0]:
+        raise RuntimeError("training scan failed: " + lib.kdecay_last_error_string().decode())
+    n = B * H * N * D
+    fus, bus = rf * 1e3 / steps, rb * 1e3 / steps
+    return {"config": "C2 shape, bf16: forward with saved states, then backward (dV, dlam)",
+            "fwd_train_us": round(fus, 3), "fwd_train_GBps": round(4 * n / (fus * 1e-6) / 1e9, 1),
+            "bwd_us": round(bus, 3), "bwd_GBps": round(6 * n / (bus * 1e-6) / 1e9, 1),
+            "bwd_pct_of_peak": round(100 * 6 * n / (bus * 1e-6) / 1e9 / HBM_PEAK_GBPS, 2)}
+
+
+def bench_e2e(torch, dev, iters=5):
+    """C5: KilatTransformer forward (768 wide, 12 layers, 6 decay + 6 MLA heads, MoE 8 x top-2,
+    vocab 50000), random init, bf16 autocast, B=8 N=1024, decay path on the HIP kernel.
+    Timed with the reference's glue (two .contiguous() copies around the op) and with
+    layout-fused I/O; the decay op's own share is timed with events around its calls."""
+    import kilat_amd
+    from kilat_amd.e2e_model import E2EConfig, KilatE2E
+
+    torch.manual_seed(4)
+    cfg = E2EConfig()
+    B, N = 8, 1024
+    spans = []
+
+    def timed_decay(lam, V):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        y = kilat_amd.triton_global_decay(lam, V)
+        b.record()
+        spans.append((a, b))
+        return y
+
+    model = KilatE2E(cfg, timed_decay).to(dev).eval()
+    ids = torch.randint(0, cfg.vocab_size, (B, N), device=dev)
+    out = {"config": "C5: n_embd=768 n_layer=12 n_head=12 recall_ratio=0.5 MoE 8 x top-2 (+2 shared) "
+                     "vocab=50000, bf16 autocast, B=8 N=1024, random init"}
+    for fused in (False, True):
+        model.set_decay(timed_decay, fused_layout=fused)
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            for _ in range(2):
+                model(ids)
+            torch.cuda.synchronize()
+            spans.clear()
+            t = time.perf_counter()
+            for _ in range(iters):
+                model(ids)
+            torch.cuda.synchronize()
+            sec = (time.perf_counter() - t) / iters
+        decay_ms = sum(a.elapsed_time(b) for a, b in spans) / iters
+        key = "fused_layout" if fused else "reference_glue"
+        out[key] = {"ms_per_forward": round(sec * 1e3, 3), "tokens_per_s": round(B * N / sec, 1),
+                    "decay_ms_per_forward": round(decay_ms, 4),
+                    "decay_share_pct": round(100 * decay_ms / (sec * 1e3), 3)}
+    return out
+
+
 def cpu_baseline(torch, B, H, N, D):
     """The oracle's torch restatement of the reference CPU path on the host cores."""
     from oracle import decay_oracle as O
@@ -307,6 +403,12 @@ def main() -> int:
         extras["decode"] = bench_decode(torch, kilat_amd, dev)
         log("long context C4")
         extras["long_context"] = bench_long(torch, kilat_amd, dev)
+        torch.cuda.empty_cache()
+        log("training forward + backward (C2 shape)")
+        extras["backward"] = bench_backward(torch, dev)
+        torch.cuda.empty_cache()
+        log("end-to-end model forward (C5)")
+        extras["e2e"] = bench_e2e(torch, dev)
     result["extras"] = extras
     if not args.no_cpu_baseline:
         log("CPU baseline (oracle restatement of the reference CPU path)")

@@ -1,0 +1,43 @@
+"""End-to-end: the KilatTransformer forward restatement (kilat_amd.e2e_model) with
+the decay path on the HIP kernel matches the same model on the CPU with the
+oracle's decay (the reference's _cpu_global_decay, triton_ops.py:232-247), on
+identical weights and tokens.  Tolerance: logits within 1e-4 relative to their
+scale (fp32; the rest of the model runs on different devices)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import kilat_amd
+from kilat_amd.e2e_model import E2EConfig, KilatE2E
+from oracle import decay_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def tiny():
+    return E2EConfig(vocab_size=256, n_embd=64, n_layer=2, n_head=4, num_experts=4, active_experts=2)
+
+
+def test_e2e_logits_match_cpu_reference_decay(hip_device, kdecay_lib):
+    torch.manual_seed(40)
+    model = KilatE2E(tiny(), O.global_decay).eval()
+    with torch.no_grad():  # vary the decay rates per head so every head differs
+        for blk in model.layers:
+            blk.attn.log_lambda.copy_(torch.randn_like(blk.attn.log_lambda) + 2.0)
+    ids = torch.randint(0, 256, (2, 700), generator=torch.Generator().manual_seed(41))
+    with torch.no_grad():
+        ref, ref_loss = model(ids, labels=ids)
+    model = model.to(hip_device)
+    out = {}
+    for fused in (False, True):
+        print(f"  e2e fused_layout={fused}", flush=True)
+        model.set_decay(kilat_amd.triton_global_decay, fused_layout=fused)
+        with torch.no_grad():
+            logits, loss = model(ids.to(hip_device), labels=ids.to(hip_device))
+        torch.cuda.synchronize()
+        out[fused] = logits.cpu()
+        err = float((logits.cpu() - ref).abs().max() / ref.abs().max())
+        assert err <= 1e-4, f"fused={fused}: logits rel err {err:.3e}"
+        assert abs(float(loss) - float(ref_loss)) <= 1e-4 * abs(float(ref_loss))
+    assert torch.equal(out[False], out[True])  # layout-fused I/O changes no value

@@ -304,3 +304,19 @@ def test_oracle_grad_dlam_and_init_finite_difference():
     im[0, 1, 2] -= eps
     fd = (_loss(lam.detach(), V, gy, ip, gfin, 4) - _loss(lam.detach(), V, gy, im, gfin, 4)) / (2 * eps)
     assert abs(float(fd) - float(init.grad[0, 1, 2])) <= 1e-6 * max(1.0, abs(float(fd)))
+
+
+def test_e2e_model_runs_on_cpu_with_oracle_decay():
+    """Host-side check of the end-to-end restatement (shapes, tied head, finite loss)."""
+    from kilat_amd.e2e_model import E2EConfig, KilatE2E
+
+    torch.manual_seed(42)
+    cfg = E2EConfig(vocab_size=128, n_embd=32, n_layer=2, n_head=4, num_experts=4, active_experts=2)
+    model = KilatE2E(cfg, O.global_decay).eval()
+    assert model.lm_head.weight is model.wte.weight
+    assert model.layers[0].attn.n_global == 2 and model.layers[0].attn.latent == 8
+    assert len(model.layers[0].mlp.shared_experts) == 2
+    ids = torch.randint(0, 128, (2, 9))
+    with torch.no_grad():
+        logits, loss = model(ids, labels=ids)
+    assert logits.shape == (2, 9, 128) and torch.isfinite(loss)
