@@ -393,8 +393,10 @@ struct ChunkScan {
 
   // Scan `item` from its loaded rows and store its outputs.  `epoch` is the
   // launch generation every workgroup read before publishing anything.
-  __device__ static void process(const ScanArgs& a, int item, uint4 (&raw)[R], float lam, unsigned epoch,
-                                 Smem& sm) {
+  // Tables, chunk reduction and look-back: st = the state before this lane's
+  // first row.
+  __device__ static void scan_chunk(const ScanArgs& a, int item, uint4 (&raw)[R], float lam, unsigned epoch,
+                                    Smem& sm, float (&st)[VW]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const bool multi = a.nchunk > 1;
     const int chunk = item / a.nstream, stream = item % a.nstream;
@@ -486,7 +488,7 @@ struct ChunkScan {
       }
     }
 
-    // Re-run the lane's rows from its true start state and store y.
+    // The lane's true start state.
     float ew[VW];  // state before this wavefront's first row, zero carry into the chunk
 #pragma unroll
     for (int j = 0; j < VW; ++j) ew[j] = 0.0f;
@@ -496,9 +498,21 @@ struct ChunkScan {
     }
     const float mg = sm.pw[g];
     const float mgw = sm.pw[gw];
-    float st[VW];
 #pragma unroll
     for (int j = 0; j < VW; ++j) st[j] = __builtin_fmaf(mg, sm.carry[ds * VW + j], __builtin_fmaf(mgw, ew[j], acc[j]));
+  }
+
+  // Re-run the lane's rows from st and store y (and the optional outputs).
+  __device__ static void store_chunk(const ScanArgs& a, int item, uint4 (&raw)[R], float lam, float (&st)[VW],
+                                     const Smem& sm) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int chunk = item / a.nstream, stream = item % a.nstream;
+    const int64_t bh = stream / a.ng, grp = stream % a.ng;
+    const int64_t b = bh / a.H, h = bh % a.H;
+    const int64_t c0 = bh * a.D + grp * DG;
+    const int ds = MAP ? lane / GW : lane % LPR, gw = MAP ? lane % GW : lane / LPR;
+    const int g = wave * GW + gw;
+    const int64_t rbase = (int64_t)chunk * L + (int64_t)g * R;
     TO* op = static_cast<TO*>(a.out) + b * a.ob + h * a.oh + grp * DG + (int64_t)ds * VW + rbase * a.on;
 #pragma unroll
     for (int i = 0; i < R; ++i) {
@@ -527,6 +541,13 @@ struct ChunkScan {
         for (int j = 0; j < VW; ++j) sp[j] = st[j];
       }
     }
+  }
+
+  __device__ static void process(const ScanArgs& a, int item, uint4 (&raw)[R], float lam, unsigned epoch,
+                                 Smem& sm) {
+    float st[VW];
+    scan_chunk(a, item, raw, lam, epoch, sm, st);
+    store_chunk(a, item, raw, lam, st, sm);
   }
 };
 
