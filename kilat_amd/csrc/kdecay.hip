@@ -514,9 +514,14 @@ struct ChunkScan {
     const int g = wave * GW + gw;
     const int64_t rbase = (int64_t)chunk * L + (int64_t)g * R;
     TO* op = static_cast<TO*>(a.out) + b * a.ob + h * a.oh + grp * DG + (int64_t)ds * VW + rbase * a.on;
+    // Rows of this lane inside the sequence, and which of them (if any) is
+    // row N-1, as 32-bit values (no 64-bit compare per row).
+    const int nvalid = a.N - rbase >= R ? R : (a.N - rbase > 0 ? (int)(a.N - rbase) : 0);
+    const int64_t fr = a.N - 1 - rbase;
+    const int ifin = a.fin != nullptr && fr >= 0 && fr < R ? (int)fr : -1;
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      if (rbase + i < a.N) {
+      if (i < nvalid) {
         float v[VW], y[VW];
         opaque(raw[i]);
         unpack16<TI>(raw[i], v);
@@ -527,7 +532,7 @@ struct ChunkScan {
           y[j] = st[j] * rz;
         }
         store_vec<TO, VW>(op + (int64_t)i * a.on, y);
-        if (a.fin && rbase + i == a.N - 1) {
+        if (i == ifin) {
 #pragma unroll
           for (int j = 0; j < VW; ++j) a.fin[c0 + ds * VW + j] = st[j];
         }
