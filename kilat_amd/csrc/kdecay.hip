@@ -268,6 +268,32 @@ __device__ void look_back(const u64* base, int c, unsigned tag_agg, unsigned tag
   }
 }
 
+// Sum of x over the 64 lanes of the wavefront, in a fixed order (the same
+// result on every run): DPP butterflies inside each row of 16 lanes, then the
+// four row sums.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+  x += dpp_f32<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp_f32<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp_f32<0x141>(x);  // row_half_mirror
+  x += dpp_f32<0x140>(x);  // row_mirror
+  const int xi = __builtin_bit_cast(int, x);
+  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 0)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 16))) +
+         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 32)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 48)));
+}
+
+// Index of the calling wavefront in its workgroup, as a wavefront-uniform
+// (scalar) value: loops and branches on it are then scalar, not exec-masked.
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
+
 // Value of `x` held K row groups below (row groups are S lanes apart, GW per
 // wavefront; lanes whose group index is below K get an unspecified value).
 // Adjacent groups of up to 16 lanes use a DPP row shift (no LDS traffic);
@@ -663,11 +689,12 @@ struct ChunkBwd {
     float rt[NW][DG];  // reverse per-wavefront totals
     float carry_s[DG]; // state before the chunk's first row
     float carry_g[DG]; // g after the chunk's last row
+    float gfin[DG];    // final-state gradient (last chunk only; zero elsewhere)
     float red[NW];     // dlam partial per wavefront
   };
 
   __device__ static void run(const BwdArgs& a, unsigned epoch, Smem& sm) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const bool multi = a.nchunk > 1;
     const int item = blockIdx.x;
     const int rc = item / a.nstream, stream = item % a.nstream;  // rc: position from the end
@@ -681,8 +708,27 @@ struct ChunkBwd {
     const int64_t rbase = row0 + (int64_t)g * R;
     const float lam = a.lam[h];
 
+    // For channel tid < DG: the forward state before the chunk's first row
+    // (saved by the forward pass, the initial state, or zero) and the
+    // final-state gradient (last chunk only, else zero).  Both loads are
+    // issued before the rows and unconditionally (a load under a branch is
+    // waited for at the branch join): a.lam stands in where there is nothing
+    // to load.
+    float cs, cf;
+    {
+      const int dc = tid < DG ? tid : DG - 1;
+      const float* cp = chunk > 0 ? a.states + ((int64_t)stream * a.nsaved + chunk) * DG + dc
+                                  : (a.init ? a.init + c0 + dc : a.lam);
+      const bool fin = rc == 0 && a.gfin != nullptr;
+      const float* fp = fin ? a.gfin + c0 + dc : a.lam;
+      cs = *cp;
+      cf = *fp;
+      if (chunk == 0 && !a.init) cs = 0.0f;
+      if (!fin) cf = 0.0f;
+    }
+
     // Rows of V and gy (rows past the end re-read row N-1; their u is zeroed
-    // below and their states are never used).
+    // and they are left out of every dlam term).
     uint4 rv[R], rg[R];
     {
       const T* vp = static_cast<const T*>(a.V) + b * a.vb + h * a.vh + grp * DG + (int64_t)ds * VW;
@@ -701,12 +747,17 @@ struct ChunkBwd {
 
     __syncthreads();
     if (tid <= G) sm.pw[tid] = pow_like_torch(lam, (int64_t)tid * R);
+    // Rows past the end get zeros, so that the passes below read the tables
+    // unconditionally (a read under a condition becomes a branch).
     for (int r = tid; r < L; r += NT) {
-      if (row0 + r < a.N) {
-        const int64_t t = a.t_offset + row0 + r;
-        sm.rz[r] = 1.0f / z_of(lam, t);
-        sm.rzp[r] = dinvz_dlam(lam, t + 1);
-      }
+      const bool in = row0 + r < a.N;
+      const int64_t t = a.t_offset + row0 + r;
+      sm.rz[r] = in ? 1.0f / z_of(lam, t) : 0.0f;
+      sm.rzp[r] = in ? dinvz_dlam(lam, t + 1) : 0.0f;
+    }
+    if (tid < DG) {
+      sm.carry_s[tid] = cs;
+      sm.gfin[tid] = cf;
     }
 
     // Lane-local forward total of v (zero carry in).
@@ -720,29 +771,35 @@ struct ChunkBwd {
 #pragma unroll
       for (int j = 0; j < VW; ++j) fa[j] = __builtin_fmaf(lam, fa[j], v[j]);
     }
-    __syncthreads();  // tables
+    __syncthreads();  // tables, forward carry
 
-    // u of every row; lane-local reverse total (zero carry from the right).
-    float u[R][VW];
-    float gfin[VW];
-    const bool has_fin = a.gfin != nullptr && rbase <= a.N - 1 && a.N - 1 < rbase + R;
+    // u_t = gy_t / z_t (+ the final-state gradient at row N-1) of row i:
+    // branch-free, so that the passes below do not materialise every u.
+    const int fin_i = a.N - 1 >= rbase && a.N - 1 < rbase + R ? (int)(a.N - 1 - rbase) : -1;
+    float gf[VW];
 #pragma unroll
-    for (int j = 0; j < VW; ++j) gfin[j] = has_fin ? a.gfin[c0 + ds * VW + j] : 0.0f;
+    for (int j = 0; j < VW; ++j) gf[j] = sm.gfin[ds * VW + j];
+    auto u_of = [&](int i, const float (&gv)[VW], float (&u)[VW]) {
+      const bool valid = rbase + i < a.N;
+      const float rz = sm.rz[g * R + i];
+#pragma unroll
+      for (int j = 0; j < VW; ++j) {
+        const float q = gv[j] * rz;
+        u[j] = i == fin_i ? q + gf[j] : (valid ? q : 0.0f);
+      }
+    };
+
+    // Lane-local reverse total of u (zero carry from the right).
     float ra[VW];
 #pragma unroll
     for (int j = 0; j < VW; ++j) ra[j] = 0.0f;
 #pragma unroll
     for (int i = R - 1; i >= 0; --i) {
-      float gv[VW];
+      float gv[VW], u[VW];
       unpack16<T>(rg[i], gv);
-      const bool valid = rbase + i < a.N;
-      const float rz = valid ? sm.rz[g * R + i] : 0.0f;
+      u_of(i, gv, u);
 #pragma unroll
-      for (int j = 0; j < VW; ++j) {
-        u[i][j] = valid ? gv[j] * rz : 0.0f;
-        if (rbase + i == a.N - 1) u[i][j] += gfin[j];
-        ra[j] = __builtin_fmaf(lam, ra[j], u[i][j]);
-      }
+      for (int j = 0; j < VW; ++j) ra[j] = __builtin_fmaf(lam, ra[j], u[j]);
     }
 
     // Scans over the row groups of the wavefront, both directions.
@@ -766,9 +823,56 @@ struct ChunkBwd {
     }
     __syncthreads();
 
-    // Carries of the chunk: the forward state from the forward pass, the
-    // reverse one by look-back over the chunks after this one.
+    // Forward states of the lane's rows, before the look-back: they depend on
+    // the forward carry only.  s_{t-1} of each row is kept for the dlam term
+    // sum_t g_t s_{t-1}, taken once g is known; sum_t gy_t d(1/z_t)/dlam s_t
+    // is taken here.
     const float mW = sm.pw[GW];
+    const float mg = sm.pw[g], mgw = sm.pw[gw];
+    const float mr = sm.pw[G - 1 - g], mrw = sm.pw[GW - 1 - gw];
+    float gh0[VW];    // g after the lane's last row, zero carry into the chunk's end
+    float sp[R][VW];  // s_{t-1} of the lane's rows
+    float dl = 0.0f;
+    {
+      float ew[VW], er[VW], st[VW];
+#pragma unroll
+      for (int j = 0; j < VW; ++j) {
+        ew[j] = 0.0f;
+        er[j] = 0.0f;
+      }
+      for (int w = 0; w < wave; ++w) {
+#pragma unroll
+        for (int j = 0; j < VW; ++j) ew[j] = __builtin_fmaf(mW, ew[j], sm.wt[w][ds * VW + j]);
+      }
+      for (int w = NW - 1; w > wave; --w) {
+#pragma unroll
+        for (int j = 0; j < VW; ++j) er[j] = __builtin_fmaf(mW, er[j], sm.rt[w][ds * VW + j]);
+      }
+#pragma unroll
+      for (int j = 0; j < VW; ++j) {
+        st[j] = __builtin_fmaf(mg, sm.carry_s[ds * VW + j], __builtin_fmaf(mgw, ew[j], xin[j]));
+        gh0[j] = __builtin_fmaf(mrw, er[j], rin[j]);
+      }
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        float v[VW], gv[VW];
+        opaque(rv[i]);
+        opaque(rg[i]);
+        unpack16<T>(rv[i], v);
+        unpack16<T>(rg[i], gv);
+        const bool valid = rbase + i < a.N;
+        const float rzp = sm.rzp[g * R + i];
+#pragma unroll
+        for (int j = 0; j < VW; ++j) {
+          sp[i][j] = st[j];
+          st[j] = __builtin_fmaf(lam, st[j], v[j]);
+          const float t = __builtin_fmaf(gv[j] * rzp, st[j], dl);
+          dl = valid ? t : dl;
+        }
+      }
+    }
+
+    // Reverse carry of the chunk by look-back over the chunks after it.
     if (wave == 0) {
       const float mL = sm.pw[G];
       const unsigned tag_agg = tag_of(epoch, 0u), tag_inc = tag_of(epoch, 1u);
@@ -783,13 +887,6 @@ struct ChunkBwd {
 #pragma unroll
           for (int w = NW - 1; w >= 0; --w) agg[q] = __builtin_fmaf(mW, agg[q], sm.rt[w][d]);
           if (rc > 0 && chunk > 0) publish(base + (int64_t)rc * DG + d, tag_agg, agg[q]);
-          float cs = 0.0f;
-          if (chunk == 0) {
-            if (a.init) cs = a.init[c0 + d];
-          } else {
-            cs = a.states[((int64_t)stream * a.nsaved + chunk) * DG + d];
-          }
-          sm.carry_s[d] = cs;
         }
       }
       if (rc > 0) look_back<W, DG, DQ>(base, rc, tag_agg, tag_inc, mL, a.hdr, cg);
@@ -813,71 +910,32 @@ struct ChunkBwd {
       }
     }
 
-    // The lane's true boundary values.
-    float st[VW], gn[VW];
-    {
-      float ew[VW], er[VW];
+    // Reverse pass with the true carry: g of every row, dV, sum_t g_t s_{t-1}.
+    float gn[VW];
 #pragma unroll
-      for (int j = 0; j < VW; ++j) {
-        ew[j] = 0.0f;
-        er[j] = 0.0f;
-      }
-      for (int w = 0; w < wave; ++w) {
-#pragma unroll
-        for (int j = 0; j < VW; ++j) ew[j] = __builtin_fmaf(mW, ew[j], sm.wt[w][ds * VW + j]);
-      }
-      for (int w = NW - 1; w > wave; --w) {
-#pragma unroll
-        for (int j = 0; j < VW; ++j) er[j] = __builtin_fmaf(mW, er[j], sm.rt[w][ds * VW + j]);
-      }
-      const float mg = sm.pw[g], mgw = sm.pw[gw];
-      const float mr = sm.pw[G - 1 - g], mrw = sm.pw[GW - 1 - gw];
-#pragma unroll
-      for (int j = 0; j < VW; ++j) {
-        st[j] = __builtin_fmaf(mg, sm.carry_s[ds * VW + j], __builtin_fmaf(mgw, ew[j], xin[j]));
-        gn[j] = __builtin_fmaf(mr, sm.carry_g[ds * VW + j], __builtin_fmaf(mrw, er[j], rin[j]));
-      }
-    }
-
-    // Reverse pass: g of every row, dV.
-    float gi[R][VW];
+    for (int j = 0; j < VW; ++j) gn[j] = __builtin_fmaf(mr, sm.carry_g[ds * VW + j], gh0[j]);
     T* dp = static_cast<T*>(a.dv) + b * a.db + h * a.dh + grp * DG + (int64_t)ds * VW + rbase * a.dn;
 #pragma unroll
     for (int i = R - 1; i >= 0; --i) {
+      float gv[VW], u[VW];
+      opaque(rg[i]);
+      unpack16<T>(rg[i], gv);
+      u_of(i, gv, u);
+      const bool valid = rbase + i < a.N;
 #pragma unroll
       for (int j = 0; j < VW; ++j) {
-        gn[j] = __builtin_fmaf(lam, gn[j], u[i][j]);
-        gi[i][j] = gn[j];
+        gn[j] = __builtin_fmaf(lam, gn[j], u[j]);
+        const float t = __builtin_fmaf(gn[j], sp[i][j], dl);
+        dl = valid ? t : dl;
       }
-      if (rbase + i < a.N) store_vec<T, VW>(dp + (int64_t)i * a.dn, gi[i]);
+      if (valid) store_vec<T, VW>(dp + (int64_t)i * a.dn, gn);
     }
     if (a.dinit && rbase == 0) {
 #pragma unroll
-      for (int j = 0; j < VW; ++j) a.dinit[c0 + ds * VW + j] = lam * gi[0][j];
+      for (int j = 0; j < VW; ++j) a.dinit[c0 + ds * VW + j] = lam * gn[j];
     }
 
-    // Forward pass: dlam terms.
-    float dl = 0.0f;
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-      float v[VW], gv[VW];
-      opaque(rv[i]);
-      opaque(rg[i]);
-      unpack16<T>(rv[i], v);
-      unpack16<T>(rg[i], gv);
-      if (rbase + i < a.N) {
-        const float rzp = sm.rzp[g * R + i];
-#pragma unroll
-        for (int j = 0; j < VW; ++j) {
-          const float s_new = __builtin_fmaf(lam, st[j], v[j]);
-          dl = __builtin_fmaf(gi[i][j], st[j], dl);
-          dl = __builtin_fmaf(gv[j] * rzp, s_new, dl);
-          st[j] = s_new;
-        }
-      }
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) dl += __shfl_xor(dl, off, 64);
+    dl = wave_sum(dl);
     if (lane == 0) sm.red[wave] = dl;
     __syncthreads();
     if (tid == 0) {
