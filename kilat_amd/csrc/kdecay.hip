@@ -627,9 +627,10 @@ struct BwdArgs {
   const float* states;  // forward states at chunk starts (ScanArgs::states layout), null if nchunk == 1
   const float* gfin;    // [B*H*D] or null: gradient of the final state
   float* dinit;         // [B*H*D] or null
-  float* partial;       // [nchunk * nstream] dlam partial per chunk (item order)
+  float* dlam;          // [H]
+  u64* partial;         // [nchunk * nstream] dlam partial per chunk (item order), epoch-tagged words
   int64_t vb, vh, vn, gb, gh, gn, db, dh, dn;
-  int64_t H, N, t_offset, D;
+  int64_t B, H, N, t_offset, D;
   int ng, nchunk, nstream;
   int64_t nsaved;
   u64* flags;
@@ -691,6 +692,7 @@ struct ChunkBwd {
     float carry_g[DG]; // g after the chunk's last row
     float gfin[DG];    // final-state gradient (last chunk only; zero elsewhere)
     float red[NW];     // dlam partial per wavefront
+    double dred[NT];   // per-thread sums of the head reduction
   };
 
   __device__ static void run(const BwdArgs& a, unsigned epoch, Smem& sm) {
@@ -901,8 +903,10 @@ struct ChunkBwd {
     }
     __syncthreads();
 
-    // Chunk 0 is the last of its stream in this order; see ChunkScan.
-    if (multi && chunk == 0 && tid == 0) {
+    // Chunk 0 is the last of its stream in this order; see ChunkScan.  (With
+    // one chunk per stream every workgroup is a chunk 0: the epoch still
+    // advances, for the dlam partials' tags.)
+    if (chunk == 0 && tid == 0) {
       const unsigned d = __hip_atomic_fetch_add(a.hdr + HDR_DONE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (d == (unsigned)a.nstream - 1u) {
         __hip_atomic_store(a.hdr + HDR_DONE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -942,13 +946,50 @@ struct ChunkBwd {
       float sum = 0.0f;
 #pragma unroll
       for (int w = 0; w < NW; ++w) sum += sm.red[w];
-      a.partial[item] = sum;
+      publish(a.partial + item, tag_of(epoch, 0u), sum);
     }
+
+    // The workgroup with the largest item index of head h sums the head's
+    // partials.  Every other item of the head has a smaller index, so it was
+    // dispatched earlier and finishes without waiting on this workgroup.
+    if (rc == a.nchunk - 1 && b == a.B - 1 && grp == a.ng - 1) reduce_head(a, h, epoch, sm);
+  }
+
+  // dlam[h] = the sum of head h's chunk partials in double, in a fixed order
+  // (strided per-thread sums, then a pairwise tree), whatever the order in
+  // which the partials arrive: deterministic.
+  __device__ static void reduce_head(const BwdArgs& a, int64_t h, unsigned epoch, Smem& sm) {
+    const int tid = threadIdx.x;
+    const unsigned tag = tag_of(epoch, 0u);
+    const int64_t n = a.B * a.ng * (int64_t)a.nchunk;
+    double acc = 0.0;
+    for (int64_t idx = tid; idx < n; idx += NT) {
+      const int64_t rc = idx % a.nchunk, bg = idx / a.nchunk;
+      const int64_t b = bg / a.ng, grp = bg % a.ng;
+      const u64* p = a.partial + rc * a.nstream + (b * a.H + h) * a.ng + grp;
+      u64 w = peek(p);
+      for (int spin = 0; (unsigned)(w >> 32) != tag; ++spin) {
+        if (spin >= kSpinLimit) {
+          __hip_atomic_store(a.hdr + HDR_ERROR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          w = (u64)tag << 32;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        w = peek(p);
+      }
+      acc += (double)__uint_as_float((unsigned)w);
+    }
+    sm.dred[tid] = acc;
+    __syncthreads();
+    for (int s = NT / 2; s >= 1; s >>= 1) {
+      if (tid < s) sm.dred[tid] += sm.dred[tid + s];
+      __syncthreads();
+    }
+    if (tid == 0) a.dlam[h] = (float)sm.dred[0];
   }
 };
 
 __device__ __forceinline__ unsigned read_epoch_bwd(const BwdArgs& a) {
-  if (a.nchunk <= 1) return 0u;
   return __hip_atomic_load(a.hdr + HDR_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -958,28 +999,6 @@ __global__ __launch_bounds__(NW * 64) void scan_bwd(BwdArgs a) {
   __shared__ typename CB::Smem sm;
   const unsigned epoch = read_epoch_bwd(a);
   CB::run(a, epoch, sm);
-}
-
-// dlam[h] = sum of the chunk partials of head h, in a fixed order, in double.
-__global__ __launch_bounds__(256) void reduce_dlam(const float* partial, float* dlam, int64_t B, int64_t H,
-                                                   int ng, int nchunk, int nstream) {
-  __shared__ double red[256];
-  const int64_t h = blockIdx.x;
-  const int64_t n = B * ng * (int64_t)nchunk;
-  double acc = 0.0;
-  for (int64_t idx = threadIdx.x; idx < n; idx += 256) {
-    const int64_t rc = idx % nchunk, bg = idx / nchunk;
-    const int64_t b = bg / ng, grp = bg % ng;
-    const int64_t stream = (b * H + h) * ng + grp;
-    acc += (double)partial[rc * nstream + stream];
-  }
-  red[threadIdx.x] = acc;
-  __syncthreads();
-  for (int s = 128; s >= 1; s >>= 1) {
-    if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) dlam[h] = (float)red[0];
 }
 
 // --------------------------------------------------------------------------
@@ -1372,7 +1391,7 @@ size_t kdecay_scan_bwd_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t 
   const int64_t nchunk = (N + Lb - 1) / Lb;
   const size_t flags = nchunk > 1 ? (size_t)(B * H * nchunk * D) * sizeof(u64) : 0;
   const int64_t nstream = B * H * (D / group_width(v_dtype, D));
-  const size_t partial = ((size_t)(nstream * nchunk) * sizeof(float) + 255) & ~(size_t)255;
+  const size_t partial = ((size_t)(nstream * nchunk) * sizeof(u64) + 255) & ~(size_t)255;
   return kHeaderBytes + flags + partial;
 }
 
@@ -1428,6 +1447,7 @@ int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides, const 
   a.states = states;
   a.gfin = g_final;
   a.dinit = d_init;
+  a.dlam = dlam;
   a.vb = v_strides[0];
   a.vh = v_strides[1];
   a.vn = v_strides[2];
@@ -1437,6 +1457,7 @@ int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides, const 
   a.db = dv_strides[0];
   a.dh = dv_strides[1];
   a.dn = dv_strides[2];
+  a.B = B;
   a.H = H;
   a.N = N;
   a.t_offset = t_offset;
@@ -1448,7 +1469,7 @@ int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides, const 
   a.hdr = static_cast<unsigned*>(workspace);
   const size_t flag_bytes = nchunk > 1 ? (size_t)(B * H * nchunk * D) * sizeof(u64) : 0;
   a.flags = nchunk > 1 ? reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes) : nullptr;
-  a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + kHeaderBytes + flag_bytes);
+  a.partial = reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes + flag_bytes);
   int e;
   if (v_dtype == KDECAY_F32)
     e = dispatch_bwd<float>(a, DG, grid, s);
@@ -1456,10 +1477,7 @@ int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides, const 
     e = dispatch_bwd<__bf16>(a, DG, grid, s);
   else
     e = dispatch_bwd<_Float16>(a, DG, grid, s);
-  if (e) return e;
-  hipLaunchKernelGGL(reduce_dlam, dim3((unsigned)H), dim3(256), 0, s, a.partial, dlam, B, H, a.ng, a.nchunk,
-                     a.nstream);
-  return hip_check("reduce_dlam launch");
+  return e;
 }
 
 int kdecay_scan_fwd_sequential(const void* V, int v_dtype, const int64_t* v_strides, void* out,
