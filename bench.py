@@ -5,8 +5,8 @@ Workload (the metric's configuration): full-sequence decay scan, bf16 V and y,
 fp32 arithmetic, B=8 N=4096 H=12 D=64 (25.2 M elements, 100.66 MB of
 algorithmic traffic per launch: one read of V, one write of y).  A step is one
 launch of the scan over one batch; inputs are resident in HBM and the step
-rotates over enough (V, y) buffer sets (400 MB) that the 256 MB Infinity Cache
-cannot hold the working set between launches.
+rotates over 8 (V, y) buffer sets (400 MB of V, 400 MB of y), so neither the
+inputs nor the outputs fit the 256 MB Infinity Cache between launches.
 
 Prints one JSON line.  Also measured (under "extras"): the box's copy
 bandwidth, the decode step (C3: 256 x 12 x 64, launch-latency bound) and the
@@ -41,7 +41,7 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--rotate", type=int, default=4, help="(V, y) buffer sets cycled through")
+    p.add_argument("--rotate", type=int, default=8, help="(V, y) buffer sets cycled through")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true")
     return p.parse_args()
@@ -125,7 +125,7 @@ def time_region(torch, launch, steps: int, warmup: int):
 
 
 def copy_bandwidth(torch, dev) -> float:
-    n = 128 * 1024 * 1024  # 256 MB of bf16 per buffer, 4 pairs rotated
+    n = 128 * 1024 * 1024  # 256 MB of bf16 per buffer
     bufs = [(torch.empty(n, dtype=torch.bfloat16, device=dev), torch.empty(n, dtype=torch.bfloat16, device=dev))
             for _ in range(2)]
     for a, b in bufs:
@@ -234,7 +234,8 @@ def bench_backward(torch, dev, steps=100):
     """C2-shaped training pass: kdecay_scan_fwd_train, then kdecay_scan_bwd (dV, dlam).
 
     Algorithmic bytes: forward 4 B/element (V in, y out); backward 6 B/element
-    (V and gy in, dV out).  3 rotated buffer sets (450 MB) keep it out of MALL.
+    (V and gy in, dV out).  4 rotated buffer sets (400 MB of V and gy) keep the
+    inputs out of the 256 MB Infinity Cache.
     """
     from kilat_amd import _lib
     from kilat_amd.triton_ops import _stream_ptr, _workspace
@@ -249,7 +250,8 @@ def bench_backward(torch, dev, steps=100):
     nbytes = max(lib.kdecay_scan_workspace_bytes(B, H, N, D, code), lib.kdecay_scan_bwd_workspace_bytes(B, H, N, D, code))
     ws = _workspace(dev, stream, nbytes)
     sets = []
-    for _ in range(3):
+    nset = 4
+    for _ in range(nset):
         V = torch.randn(B, H, N, D, generator=g, device=dev).to(torch.bfloat16)
         gy = torch.randn(B, H, N, D, generator=g, device=dev).to(torch.bfloat16)
         sets.append((V, gy, torch.empty_like(V), torch.empty_like(V), torch.empty(nst, device=dev),
@@ -258,13 +260,13 @@ def bench_backward(torch, dev, steps=100):
     rc = [0]
 
     def fwd(k):
-        V, gy, y, dV, states, dlam, fin = sets[k % 3]
+        V, gy, y, dV, states, dlam, fin = sets[k % nset]
         rc[0] |= lib.kdecay_scan_fwd_train(V.data_ptr(), code, st, y.data_ptr(), code, st, lam.data_ptr(), None,
                                            fin.data_ptr(), states.data_ptr(), nst, B, H, N, D, 0, ws.data_ptr(),
                                            ws.numel(), stream)
 
     def bwd(k):
-        V, gy, y, dV, states, dlam, fin = sets[k % 3]
+        V, gy, y, dV, states, dlam, fin = sets[k % nset]
         rc[0] |= lib.kdecay_scan_bwd(V.data_ptr(), code, st, gy.data_ptr(), st, dV.data_ptr(), st, lam.data_ptr(),
                                      None, states.data_ptr(), None, dlam.data_ptr(), None, B, H, N, D, 0,
                                      ws.data_ptr(), ws.numel(), stream)
