@@ -427,13 +427,11 @@ struct ChunkScan {
     const bool multi = a.nchunk > 1;
     const int chunk = item / a.nstream, stream = item % a.nstream;
     const int64_t bh = stream / a.ng, grp = stream % a.ng;
-    const int64_t b = bh / a.H, h = bh % a.H;
     const int64_t c0 = bh * a.D + grp * DG;  // channel 0 of this stream in [B*H*D] state arrays
     const int64_t row0 = (int64_t)chunk * L;
     const bool last = chunk == a.nchunk - 1;
     const int ds = MAP ? lane / GW : lane % LPR, gw = MAP ? lane % GW : lane / LPR;
     const int g = wave * GW + gw;
-    const int64_t rbase = row0 + (int64_t)g * R;
 
     // Per-head tables, while the rows are in flight.  (The barrier in front
     // of them measured 1.5% faster at B=8 N=4096 H=12 D=64 bf16 than none.)
