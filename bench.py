@@ -353,6 +353,54 @@ def cpu_baseline(torch, B, H, N, D):
             "seconds": round(sec, 4), "tokens_per_s": round(B * N / sec, 1)}
 
 
+def cpu_extras(torch):
+    """The same CPU restatement on BASELINE's other configurations (host cores,
+    fp32 arithmetic): C1 (the reference's CPU-op case), C3 (the incremental
+    step with the batch-shared t_pos of attention.py:344-360) and C4 (one
+    timed run of the 65,536-step loop)."""
+    from oracle import decay_oracle as O
+
+    out = {}
+    g = torch.Generator().manual_seed(0)
+    V = torch.randn(2, 6, 1024, 64, generator=g)
+    u = 0.90 + (0.999 - 0.90) * torch.rand(6, generator=g, dtype=torch.float64)
+    lam = torch.sigmoid(torch.log(u / (1 - u)).float())
+    O.global_decay(lam, V[:, :, :32])
+    times = []
+    for _ in range(3):
+        t = time.perf_counter()
+        O.global_decay(lam, V)
+        times.append(time.perf_counter() - t)
+    sec = statistics.median(times)
+    out["C1"] = {"config": "B=2 N=1024 H=6 D=64 fp32", "seconds": round(sec, 4),
+                 "tokens_per_s": round(2 * 1024 / sec, 1), "GBps": round(V.numel() * 8 / sec / 1e9, 4)}
+
+    g = torch.Generator().manual_seed(2)
+    S, H, D, steps = 256, 12, 64, 128
+    lam = c2_lam(H, torch)
+    state = torch.randn(S, H, D, generator=g)
+    vs = torch.randn(steps, S, H, D, generator=g).to(torch.bfloat16)
+    O.step(lam, state, vs[0], 100)
+    t = time.perf_counter()
+    for k in range(steps):
+        _, state = O.step(lam, state, vs[k], 1000 + k)
+    sec = time.perf_counter() - t
+    out["C3_step"] = {"config": "256 x 12 x 64, bf16 v_t, fp32 state, batch-shared t_pos, 128 steps",
+                      "us_per_step": round(sec / steps * 1e6, 2), "tokens_per_s": round(S * steps / sec, 1)}
+
+    g = torch.Generator().manual_seed(3)
+    V = torch.randn(1, 16, 65536, 128, generator=g).to(torch.bfloat16).float()
+    u = 0.99 + (0.99999 - 0.99) * torch.rand(16, generator=torch.Generator().manual_seed(3), dtype=torch.float64)
+    lam = torch.sigmoid(torch.log(u / (1 - u)).float())
+    O.global_decay(lam, V[:, :, :64])
+    t = time.perf_counter()
+    O.global_decay(lam, V)
+    sec = time.perf_counter() - t
+    out["C4"] = {"config": "B=1 N=65536 H=16 D=128 (bf16-rounded V as fp32), one run", "seconds": round(sec, 3),
+                 "tokens_per_s": round(65536 / sec, 1), "GBps": round(V.numel() * 4 / sec / 1e9, 4)}
+    return out
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -430,6 +478,9 @@ def main() -> int:
     if not args.no_cpu_baseline:
         log("CPU baseline (oracle restatement of the reference CPU path)")
         result["cpu_baseline"] = cpu_baseline(torch, B, H, N, D)
+        if not args.no_extras:
+            log("CPU restatement on C1, C3 and C4")
+            result["cpu_baseline"]["extras"] = cpu_extras(torch)
     print(json.dumps(result), flush=True)
     return 0
 
