@@ -129,3 +129,69 @@ def test_no_grad_path_unchanged(hip_device, kdecay_lib):
     y2 = kilat_amd.triton_global_decay(lam, Vg)
     torch.cuda.synchronize()
     assert y2.grad_fn is not None and torch.equal(y, y2.detach())
+
+
+@pytest.mark.parametrize("N", [100, 3000])
+def test_graph_capture_backward_replays(hip_device, kdecay_lib, N):
+    """kdecay_scan_fwd_train + kdecay_scan_bwd captured in a HIP graph: the
+    backward's dlam partials are tagged with the workspace's launch epoch, so
+    every replay, with eager launches on the same workspace between replays,
+    must reproduce the eager dV, dlam and d(init) bit for bit.  N=100 is one
+    chunk per stream (no look-back, the epoch still advances); N=3000 is 24."""
+    from kilat_amd import _lib
+    from kilat_amd.triton_ops import _stream_ptr, _workspace
+
+    lib = kdecay_lib
+    g = torch.Generator().manual_seed(31)
+    B, H, D = 2, 4, 64
+    code = _lib.KDECAY_BF16
+    lam = lam_uniform(H, 0.5, 0.999, g).to(hip_device)
+    V = torch.randn(B, H, N, D, generator=g).to(torch.bfloat16).to(hip_device)
+    gy = torch.randn(B, H, N, D, generator=g).to(torch.bfloat16).to(hip_device)
+    init = torch.randn(B, H, D, generator=g).to(hip_device)
+    gfin = torch.randn(B, H, D, generator=g).to(hip_device)
+    st = _lib.strides4(V.stride())
+    nst = lib.kdecay_scan_saved_states_floats(B, H, N, D, code)
+    y = torch.empty_like(V)
+    states = torch.empty(max(nst, 1), device=hip_device)
+    fin = torch.empty(B, H, D, device=hip_device)
+    dV = torch.empty_like(V)
+    dlam = torch.empty(H, device=hip_device)
+    dinit = torch.empty(B, H, D, device=hip_device)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+
+    def launch():
+        s = _stream_ptr(hip_device)
+        nbytes = max(lib.kdecay_scan_workspace_bytes(B, H, N, D, code),
+                     lib.kdecay_scan_bwd_workspace_bytes(B, H, N, D, code))
+        ws = _workspace(hip_device, s, nbytes)
+        wp, wn = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
+        _lib.check(lib.kdecay_scan_fwd_train(V.data_ptr(), code, st, y.data_ptr(), code, st, lam.data_ptr(),
+                                             init.data_ptr(), fin.data_ptr(), states.data_ptr() if nst else None,
+                                             nst, B, H, N, D, 5, wp, wn, s), "fwd_train")
+        _lib.check(lib.kdecay_scan_bwd(V.data_ptr(), code, st, gy.data_ptr(), st, dV.data_ptr(), st, lam.data_ptr(),
+                                       init.data_ptr(), states.data_ptr() if nst else None, gfin.data_ptr(),
+                                       dlam.data_ptr(), dinit.data_ptr(), B, H, N, D, 5, wp, wn, s), "bwd")
+
+    with torch.cuda.stream(stream):
+        launch()  # eager first: creates the workspace outside the capture
+    torch.cuda.synchronize()
+    ref = (dV.clone(), dlam.clone(), dinit.clone())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            launch()
+    torch.cuda.synchronize()
+    for r in range(4):
+        print(f"  backward graph replay {r} N={N}", flush=True)
+        dV.zero_(); dlam.zero_(); dinit.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(dV, ref[0]) and torch.equal(dlam, ref[1]) and torch.equal(dinit, ref[2]), r
+        with torch.cuda.stream(stream):
+            launch()
+        torch.cuda.synchronize()
+        assert torch.equal(dlam, ref[1]), r
+    with torch.cuda.stream(stream):
+        assert kilat_amd.workspace_error(V) == 0
