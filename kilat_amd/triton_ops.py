@@ -202,6 +202,10 @@ def global_decay_scan(
     Returns y ([B,H,N,D], dtype out_dtype or V.dtype, laid out like V), and
     with return_final_state also s_{N-1} ([B,H,D] fp32).
     algorithm: "chunked" (default) or "sequential" (the cross-check kernel).
+    Gradients (when lam, V or initial_state requires grad) need the chunked
+    scan.  The backward kernel takes the upstream gradient in V's dtype: with
+    out_dtype=float32 for a bf16/fp16 V, that gradient is rounded to V's dtype
+    first.
     """
     _require_hip(V, "V")
     if V.dim() != 4:
