@@ -204,6 +204,16 @@ const char* kdecay_version(void);
 /* Message for the calling thread's last non-zero return ("" if none). */
 const char* kdecay_last_error_string(void);
 
+/*
+ * Test hook, no counterpart in the reference: the bounded waits of later
+ * launches (chunk look-back, the backward's dlam reduction) give up after
+ * `polls` polls instead of about a second's worth, so a test can force the
+ * give-up path: the launch still returns, its output is wrong and the
+ * workspace's sticky error word is set.  polls <= 0 restores the default.
+ * Process-wide, not thread-safe; returns the previous setting (0: default).
+ */
+int kdecay_debug_set_spin_limit(int polls);
+
 #ifdef __cplusplus
 }
 #endif

@@ -37,6 +37,7 @@ EXPORTS = (
     "kdecay_step",
     "kdecay_version",
     "kdecay_last_error_string",
+    "kdecay_debug_set_spin_limit",
 )
 
 _c_i64 = ctypes.c_int64
@@ -117,6 +118,8 @@ def load() -> ctypes.CDLL:
     lib.kdecay_version.argtypes = []
     lib.kdecay_last_error_string.restype = ctypes.c_char_p
     lib.kdecay_last_error_string.argtypes = []
+    lib.kdecay_debug_set_spin_limit.restype = ctypes.c_int
+    lib.kdecay_debug_set_spin_limit.argtypes = [ctypes.c_int]
     _lib = lib
     return lib
 

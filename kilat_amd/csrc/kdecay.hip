@@ -239,7 +239,7 @@ __device__ __forceinline__ bool fold_window(const u64 (&w)[W], unsigned tag_agg,
 // lane + 64q.  Re-reads the window until every channel's fold succeeds.
 template <int W, int DG, int DQ>
 __device__ void look_back(const u64* base, int c, unsigned tag_agg, unsigned tag_inc, float mL, unsigned* hdr,
-                          float (&carry)[DQ]) {
+                          int spin_limit, float (&carry)[DQ]) {
   const int lane = threadIdx.x & 63;
   bool done[DQ];
 #pragma unroll
@@ -257,7 +257,7 @@ __device__ void look_back(const u64* base, int c, unsigned tag_agg, unsigned tag
 #pragma unroll
     for (int q = 0; q < DQ; ++q) all &= done[q];
     if (__ballot(!all) == 0ull) return;
-    if (spin >= kSpinLimit) {
+    if (spin >= spin_limit) {
       __hip_atomic_store(hdr + HDR_ERROR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
       for (int q = 0; q < DQ; ++q)
@@ -347,6 +347,7 @@ struct ScanArgs {
   float* states;
   int64_t state_rows;
   int64_t nsaved;
+  int spin_limit;  // polls before a look-back gives up (kSpinLimit unless a test lowers it)
 };
 
 // 16-byte load of data read exactly once (non-temporal: no cache residency).
@@ -487,7 +488,7 @@ struct ChunkScan {
           if (chunk > 0 && !last) publish(base + (int64_t)chunk * DG + d, tag_agg, agg[q]);
         }
       }
-      if (chunk > 0) look_back<W, DG, DQ>(base, chunk, tag_agg, tag_inc, mL, a.hdr, carry);
+      if (chunk > 0) look_back<W, DG, DQ>(base, chunk, tag_agg, tag_inc, mL, a.hdr, a.spin_limit, carry);
 #pragma unroll
       for (int q = 0; q < DQ; ++q) {
         const int d = lane + 64 * q;
@@ -633,6 +634,7 @@ struct BwdArgs {
   int64_t nsaved;
   u64* flags;
   unsigned* hdr;
+  int spin_limit;  // as ScanArgs::spin_limit, for the look-back and the dlam reduction
 };
 
 // d(1/z)/dlam for z = (1 - lam^e) / ((1 - lam) + 1e-6), evaluated in double.
@@ -889,7 +891,7 @@ struct ChunkBwd {
           if (rc > 0 && chunk > 0) publish(base + (int64_t)rc * DG + d, tag_agg, agg[q]);
         }
       }
-      if (rc > 0) look_back<W, DG, DQ>(base, rc, tag_agg, tag_inc, mL, a.hdr, cg);
+      if (rc > 0) look_back<W, DG, DQ>(base, rc, tag_agg, tag_inc, mL, a.hdr, a.spin_limit, cg);
 #pragma unroll
       for (int q = 0; q < DQ; ++q) {
         const int d = lane + 64 * q;
@@ -967,7 +969,7 @@ struct ChunkBwd {
       const u64* p = a.partial + rc * a.nstream + (b * a.H + h) * a.ng + grp;
       u64 w = peek(p);
       for (int spin = 0; (unsigned)(w >> 32) != tag; ++spin) {
-        if (spin >= kSpinLimit) {
+        if (spin >= a.spin_limit) {
           __hip_atomic_store(a.hdr + HDR_ERROR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           w = (u64)tag << 32;
           break;
@@ -1129,6 +1131,9 @@ __global__ __launch_bounds__(256) void copy_state(const float* init, float* fin,
 // --------------------------------------------------------------------------
 thread_local char g_err[512] = "";
 
+// Poll limit of the bounded waits of the next launches (kdecay_debug_set_spin_limit).
+static int g_spin_limit = kSpinLimit;
+
 int fail(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -1279,6 +1284,12 @@ const char* kdecay_version(void) { return "kdecay 0.1.0 gfx950"; }
 
 const char* kdecay_last_error_string(void) { return g_err; }
 
+int kdecay_debug_set_spin_limit(int polls) {
+  const int previous = g_spin_limit;
+  g_spin_limit = polls > 0 && polls < kSpinLimit ? polls : kSpinLimit;
+  return previous == kSpinLimit ? 0 : previous;
+}
+
 size_t kdecay_scan_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   if (B <= 0 || H <= 0 || N <= 0 || !dtype_ok(v_dtype) || !head_dim_ok(v_dtype, D)) return 0;
   const int64_t L = chunk_rows(v_dtype, D);
@@ -1341,6 +1352,7 @@ static int scan_fwd_impl(const void* V, int v_dtype, const int64_t* v_strides, v
   a.nchunk = (int)nchunk;
   a.nstream = (int)nstream;
   a.hdr = need ? static_cast<unsigned*>(workspace) : nullptr;
+  a.spin_limit = g_spin_limit;
   a.flags = need ? reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes) : nullptr;
   a.state_rows = bwd_chunk_rows(v_dtype, D);
   a.nsaved = (N + a.state_rows - 1) / a.state_rows;
@@ -1465,6 +1477,7 @@ int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides, const 
   a.nstream = (int)nstream;
   a.nsaved = nchunk;
   a.hdr = static_cast<unsigned*>(workspace);
+  a.spin_limit = g_spin_limit;
   const size_t flag_bytes = nchunk > 1 ? (size_t)(B * H * nchunk * D) * sizeof(u64) : 0;
   a.flags = nchunk > 1 ? reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes) : nullptr;
   a.partial = reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes + flag_bytes);

@@ -242,3 +242,36 @@ def test_workspace_clean_after_suite(hip_device, kdecay_lib):
     lam, V = c2_inputs(B=1, N=5000, H=2)
     gpu_scan(lam, V, hip_device)
     assert kilat_amd.workspace_error(V.to(hip_device)) == 0
+
+
+def test_lookback_give_up_is_flagged_not_hung(hip_device, kdecay_lib):
+    """Force the bounded look-back waits to give up after two polls
+    (kdecay_debug_set_spin_limit, the library's test hook): every launch still
+    returns and sets the workspace's sticky error word, and once the hook and
+    the word are cleared the same workspace serves a normal launch
+    bit-identical to the first."""
+    from kilat_amd.triton_ops import _stream_ptr, _workspaces
+
+    g = torch.Generator().manual_seed(41)
+    lam = lam_uniform(16, 0.99, 0.99999, g).to(hip_device)
+    V = torch.randn(1, 16, 32768, 128, generator=g).to(torch.bfloat16).to(hip_device)  # 64 chunks per stream
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        y_ref = kilat_amd.global_decay_scan(lam, V)
+        torch.cuda.synchronize()
+        assert kilat_amd.workspace_error(V) == 0
+        kdecay_lib.kdecay_debug_set_spin_limit(1)
+        try:
+            for k in range(3):
+                print(f"  forced give-up launch {k}", flush=True)
+                kilat_amd.global_decay_scan(lam, V)
+            torch.cuda.synchronize()
+        finally:
+            kdecay_lib.kdecay_debug_set_spin_limit(0)
+        assert kilat_amd.workspace_error(V) == 1
+        _workspaces[(hip_device.index, _stream_ptr(hip_device))][8:12].view(torch.int32).fill_(0)
+        y = kilat_amd.global_decay_scan(lam, V)
+        torch.cuda.synchronize()
+        assert kilat_amd.workspace_error(V) == 0
+    assert torch.equal(y, y_ref)
