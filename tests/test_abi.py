@@ -60,6 +60,18 @@ def test_workspace_bytes(kdecay_lib):
     assert ws(2, 6, 1024, 48, _lib.KDECAY_BF16) == 0  # unsupported D
 
 
+def test_backward_workspace_bytes(kdecay_lib):
+    wb = kdecay_lib.kdecay_scan_bwd_workspace_bytes
+    # 128-row chunks (4 rows x 4 wavefronts x 8 row groups for a 128-byte group);
+    # header + look-back words (one per channel per chunk) + one 8-byte tagged
+    # dlam partial per chunk of every stream, rounded up to 256 bytes.
+    nst, nch = 8 * 12, 4096 // 128
+    assert wb(8, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    # one chunk per stream: no look-back words, but the header and the partials
+    assert wb(2, 6, 100, 64, _lib.KDECAY_BF16) == 256 + 256
+    assert wb(2, 6, 100, 48, _lib.KDECAY_BF16) == 0  # unsupported D
+
+
 def _scan(lib, v_dtype=_lib.KDECAY_BF16, out_dtype=None, D=64, N=4096, vstr=None, ostr=None,
           V=FAKE, out=FAKE, ws=None, wsb=0):
     out_dtype = v_dtype if out_dtype is None else out_dtype
@@ -150,3 +162,15 @@ def test_integration_patches_every_module_by_name():
     assert all(m.triton_global_decay is ref_op for m in mods)
     with pytest.raises(AttributeError):
         integration.install([types.ModuleType("kilat.arc.blocks")])
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N>1 exits with a message before touching a GPU."""
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
