@@ -174,3 +174,14 @@ def test_bench_refuses_more_than_one_gpu():
                        text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_integration_doc_holds_the_tested_ctypes_stub():
+    """INTEGRATION.md's ctypes stub is the text tests/ctypes_stub.py runs on the GPU."""
+    from tests.ctypes_stub import STUB_SOURCE
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    doc = os.path.join(root, "INTEGRATION.md")
+    if not os.path.exists(doc):
+        pytest.skip("INTEGRATION.md is not in this copy of the tree")
+    assert STUB_SOURCE in open(doc).read()

@@ -275,3 +275,22 @@ def test_lookback_give_up_is_flagged_not_hung(hip_device, kdecay_lib):
         torch.cuda.synchronize()
         assert kilat_amd.workspace_error(V) == 0
     assert torch.equal(y, y_ref)
+
+
+def test_integration_ctypes_stub_matches_package(hip_device, kdecay_lib):
+    """The stand-alone ctypes stub of INTEGRATION.md gives the package's bits,
+    on a contiguous V and on the projection's strided (B,N,H*D) view."""
+    from kilat_amd import _build
+    from tests.ctypes_stub import load
+
+    stub = load(_build.LIBRARY)
+    g = torch.Generator().manual_seed(43)
+    lam = lam_uniform(6, 0.8, 0.999, g).to(hip_device)
+    V = torch.randn(2, 6, 1500, 64, generator=g).to(torch.bfloat16).to(hip_device)
+    flat = torch.randn(2, 1500, 6 * 64, generator=g).to(torch.bfloat16).to(hip_device)
+    Vs = flat.view(2, 1500, 6, 64).transpose(1, 2)
+    for x in (V, Vs):
+        ys = stub(lam, x)
+        yp = kilat_amd.triton_global_decay(lam, x)
+        torch.cuda.synchronize()
+        assert torch.equal(ys, yp)
