@@ -294,3 +294,33 @@ def test_integration_ctypes_stub_matches_package(hip_device, kdecay_lib):
         yp = kilat_amd.triton_global_decay(lam, x)
         torch.cuda.synchronize()
         assert torch.equal(ys, yp)
+
+
+def test_concurrent_streams_do_not_interfere(hip_device, kdecay_lib):
+    """Scans launched on two streams at once use one workspace per stream; their
+    launch epochs and look-back words must not mix.  Several interleaved rounds
+    on both streams, each result against its single-stream reference."""
+    g = torch.Generator().manual_seed(47)
+    lam = lam_uniform(12, 0.5, 0.9999, g).to(hip_device)
+    Va = torch.randn(4, 12, 4096, 64, generator=g).to(torch.bfloat16).to(hip_device)
+    Vb = torch.randn(2, 12, 6000, 64, generator=g).to(torch.bfloat16).to(hip_device)
+    ya_ref = kilat_amd.global_decay_scan(lam, Va)
+    yb_ref = kilat_amd.global_decay_scan(lam, Vb)
+    torch.cuda.synchronize()
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    sa.wait_stream(torch.cuda.current_stream())
+    sb.wait_stream(torch.cuda.current_stream())
+    outs = []
+    for r in range(4):
+        with torch.cuda.stream(sa):
+            ya = kilat_amd.global_decay_scan(lam, Va)
+        with torch.cuda.stream(sb):
+            yb = kilat_amd.global_decay_scan(lam, Vb)
+        outs.append((ya, yb))
+    torch.cuda.synchronize()
+    for r, (ya, yb) in enumerate(outs):
+        assert torch.equal(ya, ya_ref), r
+        assert torch.equal(yb, yb_ref), r
+    for s in (sa, sb):
+        with torch.cuda.stream(s):
+            assert kilat_amd.workspace_error(Va) == 0
