@@ -324,3 +324,21 @@ def test_concurrent_streams_do_not_interfere(hip_device, kdecay_lib):
     for s in (sa, sb):
         with torch.cuda.stream(s):
             assert kilat_amd.workspace_error(Va) == 0
+
+
+def test_native_c_abi_caller(hip_device, kdecay_lib):
+    """tests/c_abi_check.cpp: a C++ program that uses only include/kdecay.h and the
+    HIP runtime (no Python, no torch) runs the scan, the decode step and a
+    rejected argument, and checks them against its own CPU loops."""
+    import os
+    import subprocess
+
+    from tests import c_abi_build
+
+    if not os.path.exists(c_abi_build.BINARY):
+        pytest.skip("tests/_build/c_abi_check is not built (run __graft_entry__.build())")
+    print("  running tests/_build/c_abi_check", flush=True)
+    r = subprocess.run([c_abi_build.BINARY], capture_output=True, text=True, timeout=60)
+    print(r.stdout.strip(), flush=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "c_abi_check OK" in r.stdout
