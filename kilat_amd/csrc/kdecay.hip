@@ -373,7 +373,7 @@ __device__ __forceinline__ void opaque(uint4& x) {
 //
 // Items are numbered chunk-major (item = chunk * nstream + stream), so the
 // chunk an item waits on always has a smaller item number.
-template <typename TI, typename TO, int LPR, int R, int NW, int W, int MAP = 0>
+template <typename TI, typename TO, int LPR, int R, int NW, int W>
 struct ChunkScan {
   static constexpr int VW = 16 / (int)sizeof(TI);  // channels per lane
   static constexpr int DG = LPR * VW;  // channels of one stream
@@ -407,7 +407,7 @@ struct ChunkScan {
     const int64_t bh = stream / a.ng, grp = stream % a.ng;
     const int64_t b = bh / a.H, h = bh % a.H;
     const float lam = a.lam[h];
-    const int ds = MAP ? lane / GW : lane % LPR, gw = MAP ? lane % GW : lane / LPR;
+    const int ds = lane % LPR, gw = lane / LPR;
     const int64_t rbase = (int64_t)chunk * L + (int64_t)(wave * GW + gw) * R;
     const TI* vp = static_cast<const TI*>(a.V) + b * a.vb + h * a.vh + grp * DG + (int64_t)ds * VW;
 #pragma unroll
@@ -431,7 +431,7 @@ struct ChunkScan {
     const int64_t c0 = bh * a.D + grp * DG;  // channel 0 of this stream in [B*H*D] state arrays
     const int64_t row0 = (int64_t)chunk * L;
     const bool last = chunk == a.nchunk - 1;
-    const int ds = MAP ? lane / GW : lane % LPR, gw = MAP ? lane % GW : lane / LPR;
+    const int ds = lane % LPR, gw = lane / LPR;
     const int g = wave * GW + gw;
 
     // Per-head tables, while the rows are in flight.  (The barrier in front
@@ -456,7 +456,7 @@ struct ChunkScan {
     __syncthreads();  // tables
 
     // Inclusive scan over the row groups of the wavefront (adjacent lanes).
-    group_scan<1, GW, VW, MAP ? 1 : LPR>(acc, gw, sm.pw);
+    group_scan<1, GW, VW, LPR>(acc, gw, sm.pw);
     if (gw == GW - 1) {
 #pragma unroll
       for (int j = 0; j < VW; ++j) sm.wt[wave][ds * VW + j] = acc[j];
@@ -464,7 +464,7 @@ struct ChunkScan {
     // State before this lane's first row, zero carry into the wavefront.
 #pragma unroll
     for (int j = 0; j < VW; ++j) {
-      const float o = lane_shr<1, GW, MAP ? 1 : LPR>(acc[j]);
+      const float o = lane_shr<1, GW, LPR>(acc[j]);
       acc[j] = gw > 0 ? o : 0.0f;
     }
     __syncthreads();
@@ -535,7 +535,7 @@ struct ChunkScan {
     const int64_t bh = stream / a.ng, grp = stream % a.ng;
     const int64_t b = bh / a.H, h = bh % a.H;
     const int64_t c0 = bh * a.D + grp * DG;
-    const int ds = MAP ? lane / GW : lane % LPR, gw = MAP ? lane % GW : lane / LPR;
+    const int ds = lane % LPR, gw = lane / LPR;
     const int g = wave * GW + gw;
     const int64_t rbase = (int64_t)chunk * L + (int64_t)g * R;
     TO* op = static_cast<TO*>(a.out) + b * a.ob + h * a.oh + grp * DG + (int64_t)ds * VW + rbase * a.on;
@@ -592,10 +592,10 @@ __device__ __forceinline__ unsigned read_epoch(const ScanArgs& a) {
 // items with smaller indices, which are dispatched first (workgroups are
 // dispatched in index order on each XCD), so the smallest unfinished item
 // can always run: no co-residency requirement and no ticket counter.
-template <typename TI, typename TO, int LPR, int R, int NW, int W, int WPE, int MAP = 0>
+template <typename TI, typename TO, int LPR, int R, int NW, int W, int WPE>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, 8)))
 void scan_chunked(ScanArgs a) {
-  using CS = ChunkScan<TI, TO, LPR, R, NW, W, MAP>;
+  using CS = ChunkScan<TI, TO, LPR, R, NW, W>;
   __shared__ typename CS::Smem sm;
   const unsigned epoch = read_epoch(a);
   uint4 raw[R];
