@@ -64,7 +64,7 @@ def check(dv, dl, di, rdv, rdl, rdi, dtype, what):
 
 
 @pytest.mark.parametrize("dname", ["f32", "bf16", "f16"])
-@pytest.mark.parametrize("D", [16, 64, 128])
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
 def test_backward_shapes(hip_device, kdecay_lib, dname, D):
     dtype = DTYPES[dname]
     g = torch.Generator().manual_seed(200 + D)
