@@ -532,9 +532,9 @@ struct ChunkScan {
                                      const Smem& sm) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int chunk = item / a.nstream, stream = item % a.nstream;
-    const int64_t bh = stream / a.ng, grp = stream % a.ng;
-    const int64_t b = bh / a.H, h = bh % a.H;
-    const int64_t c0 = bh * a.D + grp * DG;
+    const int bh = stream / a.ng, grp = stream % a.ng;
+    const int b = bh / (int)a.H, h = bh % (int)a.H;  // 32-bit: bh < nstream
+    const int64_t c0 = (int64_t)bh * a.D + grp * DG;
     const int ds = lane % LPR, gw = lane / LPR;
     const int g = wave * GW + gw;
     const int64_t rbase = (int64_t)chunk * L + (int64_t)g * R;
@@ -701,9 +701,9 @@ struct ChunkBwd {
     const int item = blockIdx.x;
     const int rc = item / a.nstream, stream = item % a.nstream;  // rc: position from the end
     const int chunk = a.nchunk - 1 - rc;
-    const int64_t bh = stream / a.ng, grp = stream % a.ng;
-    const int64_t b = bh / a.H, h = bh % a.H;
-    const int64_t c0 = bh * a.D + grp * DG;
+    const int bh = stream / a.ng, grp = stream % a.ng;
+    const int b = bh / (int)a.H, h = bh % (int)a.H;  // 32-bit: bh < nstream
+    const int64_t c0 = (int64_t)bh * a.D + grp * DG;
     const int64_t row0 = (int64_t)chunk * L;
     const int ds = lane % LPR, gw = lane / LPR;
     const int g = wave * GW + gw;
@@ -989,8 +989,15 @@ struct ChunkBwd {
   }
 };
 
+// The launch epoch, loaded before the rows like the forward's.  The zero
+// offset comes from a vector register, so the compiler sees a per-lane value
+// and keeps it there: read through a uniform address, the value was moved to
+// a scalar register at once, which waited for the load (and so for a memory
+// round trip) before any row load was issued.
 __device__ __forceinline__ unsigned read_epoch_bwd(const BwdArgs& a) {
-  return __hip_atomic_load(a.hdr + HDR_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  unsigned zero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+  return __hip_atomic_load(a.hdr + HDR_EPOCH + zero, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <typename T, int LPR, int R, int NW, int W>
