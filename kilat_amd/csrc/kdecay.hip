@@ -288,6 +288,30 @@ __device__ __forceinline__ float wave_sum(float x) {
           __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 48)));
 }
 
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)u, CTRL, 0xf, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(u >> 32), CTRL, 0xf, 0xf, false);
+  return __builtin_bit_cast(double, ((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+  const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+  const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)u, l);
+  const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(u >> 32), l);
+  return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+
+// wave_sum in double, same fixed order.
+__device__ __forceinline__ double wave_sum_f64(double x) {
+  x += dpp_f64<0xB1>(x);
+  x += dpp_f64<0x4E>(x);
+  x += dpp_f64<0x141>(x);
+  x += dpp_f64<0x140>(x);
+  return (readlane_f64(x, 0) + readlane_f64(x, 16)) + (readlane_f64(x, 32) + readlane_f64(x, 48));
+}
+
 // Index of the calling wavefront in its workgroup, as a wavefront-uniform
 // (scalar) value: loops and branches on it are then scalar, not exec-masked.
 __device__ __forceinline__ int wave_id() {
@@ -692,7 +716,6 @@ struct ChunkBwd {
     float carry_g[DG]; // g after the chunk's last row
     float gfin[DG];    // final-state gradient (last chunk only; zero elsewhere)
     float red[NW];     // dlam partial per wavefront
-    double dred[NT];   // per-thread sums of the head reduction
   };
 
   __device__ static void run(const BwdArgs& a, unsigned epoch, Smem& sm) {
@@ -952,40 +975,48 @@ struct ChunkBwd {
     // The workgroup with the largest item index of head h sums the head's
     // partials.  Every other item of the head has a smaller index, so it was
     // dispatched earlier and finishes without waiting on this workgroup.
-    if (rc == a.nchunk - 1 && b == a.B - 1 && grp == a.ng - 1) reduce_head(a, h, epoch, sm);
+    if (rc == a.nchunk - 1 && b == a.B - 1 && grp == a.ng - 1) reduce_head(a, h, epoch);
   }
 
   // dlam[h] = the sum of head h's chunk partials in double, in a fixed order
-  // (strided per-thread sums, then a pairwise tree), whatever the order in
-  // which the partials arrive: deterministic.
-  __device__ static void reduce_head(const BwdArgs& a, int64_t h, unsigned epoch, Smem& sm) {
-    const int tid = threadIdx.x;
+  // whatever the order in which they arrive (deterministic): wavefront 0
+  // alone, each lane summing a strided subset (all its reads issued at
+  // once), then a fixed butterfly across the lanes.
+  __device__ static void reduce_head(const BwdArgs& a, int h, unsigned epoch) {
+    if (threadIdx.x >= 64) return;
+    const int lane = threadIdx.x;
     const unsigned tag = tag_of(epoch, 0u);
-    const int64_t n = a.B * a.ng * (int64_t)a.nchunk;
+    const int n = (int)a.B * a.ng * a.nchunk;
+    constexpr int K = 8;
     double acc = 0.0;
-    for (int64_t idx = tid; idx < n; idx += NT) {
-      const int64_t rc = idx % a.nchunk, bg = idx / a.nchunk;
-      const int64_t b = bg / a.ng, grp = bg % a.ng;
-      const u64* p = a.partial + rc * a.nstream + (b * a.H + h) * a.ng + grp;
-      u64 w = peek(p);
-      for (int spin = 0; (unsigned)(w >> 32) != tag; ++spin) {
-        if (spin >= a.spin_limit) {
-          __hip_atomic_store(a.hdr + HDR_ERROR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          w = (u64)tag << 32;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-        w = peek(p);
+    for (int i0 = 0; i0 < n; i0 += 64 * K) {
+      const u64* p[K];
+      u64 w[K];
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int idx = i0 + lane + 64 * k < n ? i0 + lane + 64 * k : n - 1;
+        const int rc = idx % a.nchunk, bg = idx / a.nchunk;
+        const int b = bg / a.ng, grp = bg % a.ng;
+        p[k] = a.partial + (int64_t)rc * a.nstream + ((int64_t)b * a.H + h) * a.ng + grp;
+        w[k] = peek(p[k]);
       }
-      acc += (double)__uint_as_float((unsigned)w);
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        if (i0 + lane + 64 * k >= n) continue;
+        for (int spin = 0; (unsigned)(w[k] >> 32) != tag; ++spin) {
+          if (spin >= a.spin_limit) {
+            __hip_atomic_store(a.hdr + HDR_ERROR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            w[k] = (u64)tag << 32;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+          w[k] = peek(p[k]);
+        }
+        acc += (double)__uint_as_float((unsigned)w[k]);
+      }
     }
-    sm.dred[tid] = acc;
-    __syncthreads();
-    for (int s = NT / 2; s >= 1; s >>= 1) {
-      if (tid < s) sm.dred[tid] += sm.dred[tid + s];
-      __syncthreads();
-    }
-    if (tid == 0) a.dlam[h] = (float)sm.dred[0];
+    acc = wave_sum_f64(acc);
+    if (lane == 0) a.dlam[h] = (float)acc;
   }
 };
 
