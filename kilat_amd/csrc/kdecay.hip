@@ -163,6 +163,39 @@ __device__ __forceinline__ float z_of(float lam, int64_t t) {
   return num / den;
 }
 
+// The same values with lower latency, for the decode step, where z is on the
+// critical path of a launch-latency-bound kernel: for e < 2^16 the binary
+// exponentiation is unrolled and branch-free (the same products in the same
+// order as ipow_f64; squarings past the top bit do not reach r), and the
+// small cases are selects instead of branches.  The scan kernels keep the
+// loop: they build their z tables while their rows are in flight, and there
+// the shorter form measured slower at C2 (the stores start earlier).
+__device__ __forceinline__ float pow_like_torch_fast(float x, int64_t e) {
+  double r;
+  if (e >= 0 && e < (1 << 16)) {
+    const unsigned u = (unsigned)e;
+    double xd = (double)x;
+    r = 1.0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const double rx = r * xd;
+      r = (u >> k) & 1u ? rx : r;
+      xd *= xd;
+    }
+  } else {
+    r = ipow_f64((double)x, e);
+  }
+  const float p2 = x * x;
+  const float p3 = p2 * x;
+  return e == 1 ? x : e == 2 ? p2 : e == 3 ? p3 : e == 0 ? 1.0f : (float)r;
+}
+
+__device__ __forceinline__ float z_of_fast(float lam, int64_t t) {
+  const float num = 1.0f - pow_like_torch_fast(lam, t + 1);
+  const float den = (1.0f - lam) + 1e-6f;
+  return num / den;
+}
+
 // --------------------------------------------------------------------------
 // Look-back words and the workspace header
 // --------------------------------------------------------------------------
@@ -1092,13 +1125,19 @@ __global__ __launch_bounds__(256) void decay_step(StepArgs a) {
   const int64_t bh = idx / a.D;
   const int64_t h = bh % a.H;
   const int64_t b = bh / a.H;
+  // Load order and the unconditional position load as in decay_step4.
   const float lam = a.lam[h];
+  int32_t tpv = *(a.tpos ? a.tpos + b : reinterpret_cast<const int32_t*>(a.lam));
+  __builtin_amdgcn_sched_barrier(0);
   const float s = a.s_in[idx];
   const float v = to_f32(static_cast<const TV*>(a.v)[idx]);
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" : "+v"(tpv)::"memory");
+  const int64_t tp = a.tpos ? (int64_t)tpv : a.tpos_scalar;
+  const float z = z_of_fast(lam, tp);
   const float ns = lam * s + v;  // two roundings (contraction is off)
-  const int64_t tp = a.tpos ? (int64_t)a.tpos[b] : a.tpos_scalar;
   a.s_out[idx] = ns;
-  static_cast<TO*>(a.out)[idx] = from_f32<TO>(ns / z_of(lam, tp));
+  static_cast<TO*>(a.out)[idx] = from_f32<TO>(ns / z);
 }
 
 // Four consecutive elements of T as floats / from floats (T: float, 16 bytes;
@@ -1132,17 +1171,26 @@ __device__ __forceinline__ void store4(T* p, const float (&f)[4]) {
 // thread instead of once per element.
 template <typename TV, typename TO>
 __global__ __launch_bounds__(256) void decay_step4(StepArgs a) {
-  const int64_t idx = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
-  if (idx >= a.total) return;
-  const int64_t bh = idx / a.D;
-  const int64_t h = bh % a.H;
-  const int64_t b = bh / a.H;
+  // 32-bit indices: the host launches this kernel only when total < 2^31.
+  const int idx = (int)(blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (idx >= (int)a.total) return;
+  const int bh = idx / (int)a.D;
+  const int h = bh % (int)a.H, b = bh / (int)a.H;
+  // The decay factor and position first (z needs them first, and memory
+  // operations complete in issue order), then the state and v.  The position
+  // load is unconditional (a load under a branch is waited for at the branch
+  // join, before the loads after it are issued): with no per-sequence
+  // vector it reads the decay factor's bits and discards them.
   const float lam = a.lam[h];
-  const int64_t tp = a.tpos ? (int64_t)a.tpos[b] : a.tpos_scalar;
+  int32_t tpv = *(a.tpos ? a.tpos + b : reinterpret_cast<const int32_t*>(a.lam));
+  __builtin_amdgcn_sched_barrier(0);  // keep those two loads ahead of the next two
   float s[4], v[4];
   load4<float>(a.s_in + idx, s);
   load4<TV>(static_cast<const TV*>(a.v) + idx, v);
-  const float z = z_of(lam, tp);
+  __builtin_amdgcn_sched_barrier(0);  // and all four issued before any is used
+  asm volatile("" : "+v"(tpv)::"memory");  // no use of the position moves above the loads
+  const int64_t tp = a.tpos ? (int64_t)tpv : a.tpos_scalar;
+  const float z = z_of_fast(lam, tp);
   float ns[4], o[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -1281,7 +1329,7 @@ int launch_seq(const SeqArgs& a, hipStream_t s) {
 // to its 4-element access, else one thread per element.
 template <typename TV, typename TO>
 int launch_step(const StepArgs& a, hipStream_t s) {
-  const bool vec = a.D % 4 == 0 && (uintptr_t)a.s_in % 16 == 0 && (uintptr_t)a.s_out % 16 == 0 &&
+  const bool vec = a.total < (int64_t)1 << 31 && a.D % 4 == 0 && (uintptr_t)a.s_in % 16 == 0 && (uintptr_t)a.s_out % 16 == 0 &&
                    (uintptr_t)a.v % (4 * sizeof(TV)) == 0 && (uintptr_t)a.out % (4 * sizeof(TO)) == 0;
   if (vec) {
     const int64_t nq = a.total / 4;

@@ -31,7 +31,9 @@ def test_step_scalar_tpos_bitwise(hip_device, kdecay_lib):
     g = torch.Generator().manual_seed(20)
     lam = lam_uniform(6, 0.5, 0.9999, g)
     state = torch.randn(8, 6, 64, generator=g) * 4
-    for tp in (0, 1, 2, 3, 4, 17, 1000, 65535):
+    # 65534 and 65535 straddle the kernel's switch from its unrolled power
+    # (exponent t_pos + 1 below 2^16) to the general loop.
+    for tp in (0, 1, 2, 3, 4, 17, 1000, 65534, 65535, 100000, 1 << 20, (1 << 31) + 5):
         v = torch.randn(8, 6, 64, generator=g).to(torch.bfloat16)
         print(f"  step t_pos={tp}", flush=True)
         out, ns = kilat_amd.decay_step(lam.to(hip_device), state.to(hip_device), v.to(hip_device), tp)
@@ -40,6 +42,23 @@ def test_step_scalar_tpos_bitwise(hip_device, kdecay_lib):
         assert torch.equal(ns.cpu(), rs), tp
         assert out.dtype == torch.float32 and ulps(out, ro).max() <= 1, tp
         state = rs
+
+
+def test_step_mixed_positions_in_one_wavefront(hip_device, kdecay_lib):
+    """Per-sequence positions on both sides of the unrolled-power limit in the
+    same wavefronts (4 sequences of 16 threads each share one)."""
+    g = torch.Generator().manual_seed(21)
+    lam = lam_uniform(3, 0.5, 0.9999, g)
+    tps = [0, 1, 2, 3, 4, 65534, 65535, 70000, 5, 1 << 18, 123, 65533, 9, 65536, 2, 40000]
+    B = len(tps)
+    state = torch.randn(B, 3, 64, generator=g) * 4
+    v = torch.randn(B, 3, 64, generator=g).to(torch.bfloat16)
+    tpos = torch.tensor(tps, dtype=torch.int32)
+    out, ns = kilat_amd.decay_step(lam.to(hip_device), state.to(hip_device), v.to(hip_device), tpos.to(hip_device))
+    ro, rs = O.step(lam, state, v, tps)
+    torch.cuda.synchronize()
+    assert torch.equal(ns.cpu(), rs)
+    assert ulps(out, ro).max() <= 1
 
 
 def test_c3_decode_128_steps_bitwise_state(hip_device, kdecay_lib):
