@@ -78,6 +78,24 @@ def test_backward_shapes(hip_device, kdecay_lib, dname, D):
         check(dv, dl, None, rdv, rdl, None, dtype, f"D={D} N={N}")
 
 
+@pytest.mark.parametrize("dname,H,D", [("f32", 4, 64), ("bf16", 2, 128)])
+def test_backward_long_sequence(hip_device, kdecay_lib, dname, H, D):
+    """N = 65536: 512 backward chunks per stream, so the reverse look-back
+    runs 512 chunks deep and each head's dlam sums 1024 chunk partials (two
+    rounds of the reducing wavefront's reads), against the fp64 adjoint
+    recurrence (oracle.decay_oracle.scan_grads_f64)."""
+    dtype = DTYPES[dname]
+    g = torch.Generator().manual_seed(210 + D)
+    lam = lam_uniform(H, 0.9, 0.9999, g)
+    N = 65536
+    V = torch.randn(1, H, N, D, generator=g).to(dtype)
+    gy = torch.randn(1, H, N, D, generator=g).to(dtype)
+    dv, dl, _ = gpu_grads(lam, V, gy, hip_device)
+    rdv, rdl, _ = O.scan_grads_f64(lam, V, gy)
+    assert dv.dtype == dtype
+    check(dv, dl, None, rdv, rdl, None, dtype, f"N={N} D={D} {dname}")
+
+
 def test_backward_init_final_offset(hip_device, kdecay_lib):
     g = torch.Generator().manual_seed(210)
     lam = lam_uniform(4, 0.8, 0.9999, g)

@@ -306,6 +306,32 @@ def test_oracle_grad_dlam_and_init_finite_difference():
     assert abs(float(fd) - float(init.grad[0, 1, 2])) <= 1e-6 * max(1.0, abs(float(fd)))
 
 
+@pytest.mark.parametrize("case", ["plain", "init_gfin_offset"])
+def test_adjoint_grads_match_autograd(case):
+    """scan_grads_f64 (the adjoint recurrence, for lengths autograd's graph
+    cannot hold) against fp64 autograd through the scan restatement, which the
+    two tests above pin to a closed form and to finite differences."""
+    g = torch.Generator().manual_seed(32)
+    lam = lam_uniform(3, 0.5, 0.999, g)
+    V = torch.randn(2, 3, 41, 5, generator=g)
+    gy = torch.randn(2, 3, 41, 5, generator=g)
+    init = gfin = None
+    t_offset = 0
+    if case != "plain":
+        init = torch.randn(2, 3, 5, generator=g)
+        gfin = torch.randn(2, 3, 5, generator=g)
+        t_offset = 7
+    lam64 = lam.double().requires_grad_(True)
+    V64 = V.double().requires_grad_(True)
+    init64 = init.double().requires_grad_(True) if init is not None else None
+    _loss(lam64, V64, gy.double(), init64, gfin.double() if gfin is not None else None, t_offset).backward()
+    dv, dl, di = O.scan_grads_f64(lam, V, gy, init_state=init, gfin=gfin, t_offset=t_offset)
+    assert torch.allclose(dv, V64.grad, rtol=1e-12, atol=1e-13)
+    assert torch.allclose(dl, lam64.grad, rtol=1e-11, atol=0)
+    if init is not None:
+        assert torch.allclose(di, init64.grad, rtol=1e-12, atol=1e-13)
+
+
 def test_e2e_model_runs_on_cpu_with_oracle_decay():
     """Host-side check of the end-to-end restatement (shapes, tied head, finite loss)."""
     from kilat_amd.e2e_model import E2EConfig, KilatE2E
