@@ -169,7 +169,7 @@ __device__ __forceinline__ float z_of(float lam, int64_t t) {
 // order as ipow_f64; squarings past the top bit do not reach r), and the
 // small cases are selects instead of branches.  The scan kernels keep the
 // loop: they build their z tables while their rows are in flight, and there
-// the shorter form measured slower at C2 (the stores start earlier).
+// the shorter form measured 3.7% slower (bf16, B=8 N=4096 H=12 D=64).
 __device__ __forceinline__ float pow_like_torch_fast(float x, int64_t e) {
   double r;
   if (e >= 0 && e < (1 << 16)) {
