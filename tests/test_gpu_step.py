@@ -137,6 +137,26 @@ def test_scan_then_steps_continue_the_sequence(hip_device, kdecay_lib):
     assert float(((s.cpu() - sref).abs().amax() / sref.abs().amax())) <= 1e-5
 
 
+def test_step_after_beam_reorder(hip_device, kdecay_lib):
+    """Beam search reorders each layer's cached state with index_select(0, beam_idx)
+    (/root/reference/src/kilat/pipeline/generation/generation_mixin.py:162-198).
+    The state stays fp32 [B,H,D] contiguous, so the step after a reorder is the
+    reference's step on the reordered state, bit for bit."""
+    g = torch.Generator().manual_seed(23)
+    lam = lam_uniform(4, 0.5, 0.999, g)
+    V = torch.randn(6, 4, 300, 64, generator=g).to(torch.bfloat16)
+    dev = hip_device
+    _, s = kilat_amd.global_decay_scan(lam.to(dev), V.to(dev), return_final_state=True)
+    beam_idx = torch.tensor([2, 2, 0, 5, 1, 1])
+    s_re = s.index_select(0, beam_idx.to(dev))
+    v = torch.randn(6, 4, 64, generator=g).to(torch.bfloat16)
+    out, ns = kilat_amd.decay_step(lam.to(dev), s_re, v.to(dev), 300)
+    torch.cuda.synchronize()
+    ro, rs = O.step(lam, s.cpu().index_select(0, beam_idx), v, 300)
+    assert torch.equal(ns.cpu(), rs)
+    assert ulps(out, ro).max() <= 1
+
+
 def test_step_scalar_fallback_layouts(hip_device, kdecay_lib):
     """Head dims that are not a multiple of 4, and a misaligned state, use the
     one-element-per-thread kernel; results are the same bits."""
