@@ -82,8 +82,9 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> Optional[torch
 def workspace_error(V: torch.Tensor, clear: bool = False) -> int:
     """Sticky error word of the workspace used for V's device and current stream.
 
-    0: no fault.  1: a look-back of some earlier launch gave up waiting (that
-    launch's output is wrong).  clear=True zeroes the whole workspace after
+    0: no fault.  1: a bounded wait of some earlier launch gave up (a
+    look-back, or the backward's wait for a head's dlam partials): that
+    launch's output is wrong.  clear=True zeroes the whole workspace after
     reading it (the word stays set until then).  Synchronises the stream.
     """
     ws = _workspaces.get((V.device.index, _stream_ptr(V.device)))

@@ -96,6 +96,38 @@ def test_backward_long_sequence(hip_device, kdecay_lib, dname, H, D):
     check(dv, dl, None, rdv, rdl, None, dtype, f"N={N} D={D} {dname}")
 
 
+def test_backward_give_up_is_flagged_not_hung(hip_device, kdecay_lib):
+    """Force the backward's bounded waits (the reverse look-back and the wait
+    for a head's dlam partials) to give up after one poll, through the
+    library's test hook: every launch still returns and sets the workspace's
+    sticky error word, and once the hook and the word are cleared the same
+    workspace gives gradients bit-identical to the first run."""
+    from kilat_amd.triton_ops import _stream_ptr, _workspaces
+
+    g = torch.Generator().manual_seed(43)
+    lam = lam_uniform(4, 0.9, 0.9999, g)
+    V = torch.randn(2, 4, 16384, 64, generator=g).to(torch.bfloat16)  # 128 backward chunks per stream
+    gy = torch.randn(2, 4, 16384, 64, generator=g).to(torch.bfloat16)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        dv0, dl0, _ = gpu_grads(lam, V, gy, hip_device)
+        probe = V[:, :, :1].to(hip_device)  # selects the workspace of this device and stream
+        assert kilat_amd.workspace_error(probe) == 0
+        kdecay_lib.kdecay_debug_set_spin_limit(1)
+        try:
+            for k in range(3):
+                print(f"  forced give-up backward {k}", flush=True)
+                gpu_grads(lam, V, gy, hip_device)
+        finally:
+            kdecay_lib.kdecay_debug_set_spin_limit(0)
+        assert kilat_amd.workspace_error(probe) == 1
+        _workspaces[(hip_device.index, _stream_ptr(hip_device))][8:12].view(torch.int32).fill_(0)
+        dv1, dl1, _ = gpu_grads(lam, V, gy, hip_device)
+        assert kilat_amd.workspace_error(probe) == 0
+    assert torch.equal(dv1, dv0) and torch.equal(dl1, dl0)
+
+
 def test_backward_init_final_offset(hip_device, kdecay_lib):
     g = torch.Generator().manual_seed(210)
     lam = lam_uniform(4, 0.8, 0.9999, g)
