@@ -1259,11 +1259,49 @@ bool dtype_ok(int dt) { return dt == KDECAY_F32 || dt == KDECAY_BF16 || dt == KD
 // Launch shape of the chunked scan: a chunk holds NW * 64 lanes x R rows x
 // 16 bytes = 64 KiB of input whatever the dtype and D, in 64 VGPRs per lane.
 // Measured on MI355X at B=8 N=4096 H=12 D=64 and B=1 N=65536 H=16 D=128 bf16
-// against R in {2..32}, NW in {2,4,8}, W in {2,4,8,16}: this is the fastest.
+// against R in {2..32}, NW in {2,4,8}: this is the fastest.
 constexpr int kR = 16;
 constexpr int kNW = 4;
-constexpr int kW = 4;
 constexpr int kWPE = 2;
+
+// Look-back window.  When every workgroup of a launch is resident at once, a
+// wider window resolves the chunk chains in fewer polls; when the launch runs
+// in several rounds, the chunks a workgroup waits on have mostly finished in
+// an earlier round, and reading fewer words per poll wins.  Measured (bf16,
+// same-box A/B): B=8 N=4096 H=12 D=64 (768 chunks, one round) window 4
+// 18.3 us, 2 18.5 us; B=1 N=65536 H=16 D=128 (4096 chunks, four rounds)
+// window 4 96.0 us, 3 94.5 us, 2 93.4 us.
+constexpr int kW = 4;        // the whole grid resident at once
+constexpr int kWRounds = 2;  // several rounds
+
+// Compute units of the current device, cached per device (0 if unknown).
+int cu_count() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  if (dev >= 0 && dev < 64 && __atomic_load_n(&cached[dev], __ATOMIC_RELAXED) > 0)
+    return __atomic_load_n(&cached[dev], __ATOMIC_RELAXED);
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  if (dev >= 0 && dev < 64) __atomic_store_n(&cached[dev], n, __ATOMIC_RELAXED);
+  return n;
+}
+
+// Workgroups of `kernel` that one compute unit holds at once (0 if unknown).
+int workgroups_per_cu(const void* kernel, int block) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, block, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return n;
+}
 
 // Channels of one stream: a head's row is split into groups of at most 128
 // bytes (64 bf16/fp16 or 32 fp32 channels).
@@ -1284,11 +1322,18 @@ bool head_dim_ok(int v_dtype, int64_t D) {
   return group_width(v_dtype, D) >= vw && D % group_width(v_dtype, D) == 0;
 }
 
-template <typename TI, typename TO, int DG, int R = kR, int NW = kNW, int W = kW, int WPE = kWPE>
+template <typename TI, typename TO, int DG, int R = kR, int NW = kNW, int WPE = kWPE>
 int launch_chunked(const ScanArgs& a, int64_t grid, hipStream_t s) {
   constexpr int VW = 16 / (int)sizeof(TI);
   constexpr int LPR = DG / VW;
-  hipLaunchKernelGGL((scan_chunked<TI, TO, LPR, R, NW, W, WPE>), dim3((unsigned)grid), dim3(NW * 64), 0, s, a);
+  auto* const one_round = scan_chunked<TI, TO, LPR, R, NW, kW, WPE>;
+  auto* const rounds = scan_chunked<TI, TO, LPR, R, NW, kWRounds, WPE>;
+  static const int per_cu = workgroups_per_cu(reinterpret_cast<const void*>(one_round), NW * 64);
+  const int64_t resident = (int64_t)per_cu * cu_count();
+  if (resident > 0 && grid > resident)
+    hipLaunchKernelGGL(rounds, dim3((unsigned)grid), dim3(NW * 64), 0, s, a);
+  else
+    hipLaunchKernelGGL(one_round, dim3((unsigned)grid), dim3(NW * 64), 0, s, a);
   return hip_check("scan_chunked launch");
 }
 
@@ -1306,10 +1351,12 @@ int dispatch_dg(const ScanArgs& a, int64_t DG, int64_t grid, hipStream_t s) {
 }
 
 // Launch shape of the backward scan: 4 rows per lane (it holds V, gy and g
-// of its rows in registers), 4 wavefronts.
+// of its rows in registers), 4 wavefronts, a look-back window of 2 (it runs
+// in several rounds; see kWRounds: 2-3% faster than 4 at B=8 N=4096 H=12
+// D=64 bf16, window 1 or 3 slower).
 constexpr int kRB = 4;
 constexpr int kNWB = 4;
-constexpr int kWB = 4;
+constexpr int kWB = 2;
 
 int64_t bwd_chunk_rows(int v_dtype, int64_t D) {
   const int64_t vw = 16 / elem_size(v_dtype);
