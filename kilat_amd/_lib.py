@@ -124,8 +124,19 @@ def load() -> ctypes.CDLL:
     return lib
 
 
+_strides_cache: dict = {}
+
+
 def strides4(strides) -> ctypes.Array:
-    return (ctypes.c_int64 * 4)(*[int(s) for s in strides])
+    """int64[4] strides for the C ABI, cached per stride tuple (the library
+    reads them during the call only, so one array can serve every call)."""
+    key = tuple(strides)
+    arr = _strides_cache.get(key)
+    if arr is None:
+        if len(_strides_cache) > 1024:
+            _strides_cache.clear()
+        arr = _strides_cache[key] = (ctypes.c_int64 * 4)(*[int(s) for s in key])
+    return arr
 
 
 def check(rc: int, what: str) -> None:

@@ -17,6 +17,7 @@ not patched by kilat_amd.integration and keeps Kilat's own function.)
 """
 from __future__ import annotations
 
+import contextlib
 from typing import Optional, Tuple, Union
 
 import torch
@@ -59,13 +60,41 @@ def _vector_layout_ok(t: torch.Tensor) -> bool:
     vw = 16 // t.element_size()
     if t.data_ptr() % 16:
         return False
+    if t.is_contiguous():  # every stride is a multiple of D
+        return t.size(3) % vw == 0 or t.size(0) * t.size(1) * t.size(2) <= 1
     if t.size(3) > 1 and t.stride(3) != 1:
         return False
     return all(t.size(k) == 1 or t.stride(k) % vw == 0 for k in range(3))
 
 
-def _stream_ptr(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+if hasattr(torch._C, "_cuda_getCurrentRawStream"):
+    def _stream_ptr(device: torch.device) -> int:
+        """The raw handle of torch's current stream on `device`."""
+        return torch._C._cuda_getCurrentRawStream(device.index)
+else:  # pragma: no cover - the public route, one Stream object per call
+    def _stream_ptr(device: torch.device) -> int:
+        return torch.cuda.current_stream(device).cuda_stream
+
+
+_SAME_DEVICE = contextlib.nullcontext()
+
+
+def _on_device(device: torch.device):
+    """torch.cuda.device(device), or nothing when it is already current."""
+    return _SAME_DEVICE if device.index == torch.cuda.current_device() else torch.cuda.device(device)
+
+
+_ws_bytes_cache: dict = {}
+
+
+def _fwd_workspace_bytes(lib, B: int, H: int, N: int, D: int, v_code: int) -> int:
+    key = (B, H, N, D, v_code)
+    n = _ws_bytes_cache.get(key)
+    if n is None:
+        if len(_ws_bytes_cache) > 1024:
+            _ws_bytes_cache.clear()
+        n = _ws_bytes_cache[key] = lib.kdecay_scan_workspace_bytes(B, H, N, D, v_code)
+    return n
 
 
 def _workspace(device: torch.device, stream: int, nbytes: int) -> Optional[torch.Tensor]:
@@ -100,6 +129,8 @@ def _lam32(lam: torch.Tensor, H: int, device: torch.device) -> torch.Tensor:
     _require_hip(lam, "lam_scores")
     if lam.numel() != H:
         raise ValueError(f"kilat_amd: lam_scores has {lam.numel()} elements, V has {H} heads")
+    if lam.dtype == torch.float32 and lam.dim() == 1 and lam.is_contiguous() and lam.device == device:
+        return lam  # only its memory is read
     return lam.detach().reshape(H).to(device=device, dtype=torch.float32).contiguous()
 
 
@@ -126,7 +157,7 @@ class _ScanFn(torch.autograd.Function):
         lib = _lib.load()
         nst = lib.kdecay_scan_saved_states_floats(B, H, N, D, v_code)
         states = torch.empty(max(nst, 1), dtype=torch.float32, device=dev)
-        with torch.cuda.device(dev):
+        with _on_device(dev):
             stream = _stream_ptr(dev)
             nbytes = max(lib.kdecay_scan_workspace_bytes(B, H, N, D, v_code),
                          lib.kdecay_scan_bwd_workspace_bytes(B, H, N, D, v_code))
@@ -162,7 +193,7 @@ class _ScanFn(torch.autograd.Function):
         dinit = torch.empty((B, H, D), dtype=torch.float32, device=dev) if ctx.has_init else None
         g_fin = gfin.to(torch.float32).contiguous() if gfin is not None else None
         lib = _lib.load()
-        with torch.cuda.device(dev):
+        with _on_device(dev):
             stream = _stream_ptr(dev)
             nbytes = lib.kdecay_scan_bwd_workspace_bytes(B, H, N, D, v_code)
             ws = _workspace(dev, stream, nbytes)
@@ -237,7 +268,7 @@ def global_decay_scan(
         raise ValueError(f"kilat_amd: unknown algorithm {algorithm!r}")
 
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _on_device(dev):
         stream = _stream_ptr(dev)
         init_p = init32.data_ptr() if init32 is not None else None
         fin_p = final.data_ptr() if final is not None else None
@@ -251,7 +282,7 @@ def global_decay_scan(
         else:
             Vk = V if _vector_layout_ok(V) else V.contiguous()
             outk = out if _vector_layout_ok(out) else torch.empty(V.shape, dtype=out.dtype, device=dev)
-            nbytes = lib.kdecay_scan_workspace_bytes(B, H, N, D, v_code)
+            nbytes = _fwd_workspace_bytes(lib, B, H, N, D, v_code)
             ws = _workspace(dev, stream, nbytes)
             rc = lib.kdecay_scan_fwd(
                 Vk.data_ptr(), v_code, _lib.strides4(Vk.stride()),
@@ -363,7 +394,7 @@ def decay_step(
     else:
         tpos_scalar = int(t_pos)
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _on_device(dev):
         rc = lib.kdecay_step(
             lam32.data_ptr(), s_in.data_ptr(), vk.data_ptr(), v_code,
             new_state.data_ptr(), out.data_ptr(), o_code,
