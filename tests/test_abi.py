@@ -51,12 +51,15 @@ def test_version(kdecay_lib):
 def test_workspace_bytes(kdecay_lib):
     ws = kdecay_lib.kdecay_scan_workspace_bytes
     # A stream is a (b,h) pair and a 128-byte channel group; a chunk holds 64 KiB of
-    # input: 512 rows of a 128-byte group.  Words: one per channel per chunk.
-    assert ws(8, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + 8 * 12 * 8 * 64 * 8
-    assert ws(2, 6, 512, 64, _lib.KDECAY_BF16) == 0  # one chunk per stream
-    assert ws(2, 6, 1024, 64, _lib.KDECAY_F32) == 256 + 2 * 6 * 2 * 64 * 8  # 2 groups of 32
-    assert ws(1, 16, 65536, 128, _lib.KDECAY_BF16) == 256 + 16 * 128 * 128 * 8
-    assert ws(1, 2, 4096, 32, _lib.KDECAY_BF16) == 256 + 2 * 4 * 32 * 8  # 32-channel rows: 1024-row chunks
+    # input: 512 rows of a 128-byte group, or half that (8 rows per lane instead of
+    # 16) when the 16-row grid has at most 512 chunks.  Words: one per channel per chunk.
+    assert ws(8, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + 8 * 12 * 8 * 64 * 8  # 768 chunks
+    assert ws(1, 16, 65536, 128, _lib.KDECAY_BF16) == 256 + 16 * 128 * 128 * 8  # 4096 chunks
+    assert ws(2, 6, 512, 64, _lib.KDECAY_BF16) == 256 + 2 * 6 * 2 * 64 * 8  # small grid: 256-row chunks
+    assert ws(2, 6, 256, 64, _lib.KDECAY_BF16) == 0  # one chunk per stream
+    assert ws(2, 6, 1024, 64, _lib.KDECAY_F32) == 256 + 2 * 6 * 4 * 64 * 8  # 2 groups of 32, 256-row chunks
+    assert ws(1, 2, 4096, 32, _lib.KDECAY_BF16) == 256 + 2 * 8 * 32 * 8  # 32-channel rows: 512-row chunks
+    assert ws(8, 12, 2048, 64, _lib.KDECAY_BF16) == 256 + 8 * 12 * 8 * 64 * 8  # 384 chunks at 16 rows: 8
     assert ws(2, 6, 1024, 48, _lib.KDECAY_BF16) == 0  # unsupported D
 
 

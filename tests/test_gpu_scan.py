@@ -22,12 +22,13 @@ pytestmark = pytest.mark.gpu
 DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
 
 
-def chunk_rows(dtype, D):
+def chunk_rows(dtype, D, rows_per_lane=16):
     """Rows per chunk of the library's scan: 256 lanes x 16 rows x 16 bytes of one
-    channel group of at most 128 bytes."""
+    channel group of at most 128 bytes (8 rows per lane when the 16-row grid has
+    at most 512 chunks)."""
     es = torch.empty((), dtype=dtype).element_size()
     dg = min(D, 128 // es)
-    return 4 * (64 // (dg // (16 // es))) * 16
+    return 4 * (64 // (dg // (16 // es))) * rows_per_lane
 
 
 def gpu_scan(lam, V, dev, **kw):
@@ -49,16 +50,38 @@ def assert_parity(y, ref, dtype, what=""):
 @pytest.mark.parametrize("dname", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
 def test_scan_shapes(hip_device, kdecay_lib, dname, D):
+    """Small grids (B=2, H=3): the 8-rows-per-lane kernels."""
     dtype = DTYPES[dname]
-    L = chunk_rows(dtype, D)
+    L = chunk_rows(dtype, D, 8)
     g = torch.Generator().manual_seed(100 + D)
     lam = lam_uniform(3, 0.5, 0.9999, g)
-    for N in sorted({1, 37, L - 1, L, L + 1, 3 * L + 5}):
+    for N in sorted({1, 37, L - 1, L, L + 1, 2 * L, 3 * L + 5, 6 * L + 1}):
         V = torch.randn(2, 3, N, D, generator=g).to(dtype)
         y, fin = gpu_scan(lam, V, hip_device, return_final_state=True)
         ref, sref = O.scan(lam, V)
         assert y.dtype == dtype and y.shape == V.shape
         assert_parity(y, ref, dtype, f"N={N}")
+        assert rel_err(fin, sref) <= 1e-5, f"final state N={N}"
+
+
+@pytest.mark.parametrize("dname", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
+def test_scan_shapes_large_grid(hip_device, kdecay_lib, dname, D):
+    """Grids of more than 512 chunks at 16 rows per lane: the 16-row kernels,
+    with a ragged last chunk and a chunk boundary at the end."""
+    dtype = DTYPES[dname]
+    es = torch.empty((), dtype=dtype).element_size()
+    ng = D // min(D, 128 // es)
+    L = chunk_rows(dtype, D, 16)
+    H = 8
+    B = -(-300 // (H * ng))  # at least 300 streams: 2 chunks each exceed 512
+    g = torch.Generator().manual_seed(150 + D)
+    lam = lam_uniform(H, 0.5, 0.9999, g)
+    for N in (L + 5, 2 * L):
+        V = torch.randn(B, H, N, D, generator=g).to(dtype)
+        y, fin = gpu_scan(lam, V, hip_device, return_final_state=True)
+        ref, sref = O.scan(lam, V)
+        assert_parity(y, ref, dtype, f"N={N} B={B}")
         assert rel_err(fin, sref) <= 1e-5, f"final state N={N}"
 
 
