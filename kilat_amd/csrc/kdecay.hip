@@ -14,7 +14,8 @@
 // pass by decoupled look-back: every chunk publishes its aggregate, then its
 // inclusive prefix, as 64-bit words (tag << 32 | float bits), one word per
 // channel, so a reader needs no fence: the tag and the value arrive together.
-// Workgroups are numbered chunk-major, so a chunk only waits on workgroups
+// Workgroups are numbered chunk-major (streams rotated per chunk row, to
+// spread each stream over the XCDs), so a chunk only waits on workgroups
 // with smaller indices.  The inclusive prefix of chunk c is always the same
 // left fold
 //     F(c) = lam^L * F(c-1) + agg(c)
@@ -1257,9 +1258,10 @@ int elem_size(int dt) { return dt == KDECAY_F32 ? 4 : 2; }
 bool dtype_ok(int dt) { return dt == KDECAY_F32 || dt == KDECAY_BF16 || dt == KDECAY_F16; }
 
 // Launch shape of the chunked scan: a chunk holds NW * 64 lanes x R rows x
-// 16 bytes = 64 KiB of input whatever the dtype and D, in 64 VGPRs per lane.
-// Measured on MI355X at B=8 N=4096 H=12 D=64 and B=1 N=65536 H=16 D=128 bf16
-// against R in {2..32}, NW in {2,4,8}: this is the fastest.
+// 16 bytes = 64 KiB of input whatever the dtype and D, in 64 VGPRs per lane
+// (half that for small grids; see rows_per_lane).  Measured on MI355X at B=8
+// N=4096 H=12 D=64 and B=1 N=65536 H=16 D=128 bf16 against R in {2..32}, NW
+// in {2,4,8}: this is the fastest.
 constexpr int kR = 16;
 constexpr int kNW = 4;
 constexpr int kWPE = 2;
