@@ -136,10 +136,12 @@ def test_chunked_vs_sequential_kernel(hip_device, kdecay_lib):
     assert rel_err(y, ys) <= 1e-5
 
 
-def test_layout_fused_strided_view(hip_device, kdecay_lib):
-    """V as the (B,N,H*D) projection viewed as (B,H,N,D): no contiguous() copy."""
+@pytest.mark.parametrize("B,N,H", [(2, 700, 6), (16, 2000, 12)])
+def test_layout_fused_strided_view(hip_device, kdecay_lib, B, N, H):
+    """V as the (B,N,H*D) projection viewed as (B,H,N,D): no contiguous() copy
+    (a small grid: 256-row chunks; and 768 chunks: 512-row chunks)."""
     g = torch.Generator().manual_seed(7)
-    B, N, H, D = 2, 700, 6, 64
+    D = 64
     lam = lam_uniform(H, 0.8, 0.999, g)
     flat = torch.randn(B, N, H * D, generator=g).to(torch.bfloat16).to(hip_device)
     V = flat.view(B, N, H, D).transpose(1, 2)
