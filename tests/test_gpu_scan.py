@@ -174,8 +174,9 @@ def test_unsupported_head_dim_uses_sequential_kernel(hip_device, kdecay_lib):
     assert_parity(y, O.global_decay(lam, V), torch.float32, "D=48")
 
 
-def test_fp32_output_for_bf16_input(hip_device, kdecay_lib):
-    lam, V = c2_inputs(B=1, N=3000, H=4)
+@pytest.mark.parametrize("B,H", [(1, 4), (16, 8)])
+def test_fp32_output_for_bf16_input(hip_device, kdecay_lib, B, H):
+    lam, V = c2_inputs(B=B, N=3000, H=H)  # 24 and 768 chunks at 512 rows
     y = gpu_scan(lam, V, hip_device, out_dtype=torch.float32)
     ref, _ = O.scan(lam, V, out_dtype=torch.float32)
     assert y.dtype == torch.float32
@@ -183,9 +184,12 @@ def test_fp32_output_for_bf16_input(hip_device, kdecay_lib):
 
 
 @pytest.mark.parametrize("dname", ["f32", "bf16"])
-def test_chunked_prefill_with_carry(hip_device, kdecay_lib, dname):
+@pytest.mark.parametrize("B,H", [(2, 3), (24, 8)])
+def test_chunked_prefill_with_carry(hip_device, kdecay_lib, dname, B, H):
+    """Split prefill with a carried state and a position offset, on small grids
+    and on grids of more than 512 chunks (the two chunk sizes)."""
     dtype = DTYPES[dname]
-    lam, V = c1_inputs(B=2, N=1500, H=3, D=64)
+    lam, V = c1_inputs(B=B, N=1500, H=H, D=64)
     V = V.to(dtype)
     y, s = gpu_scan(lam, V, hip_device, return_final_state=True)
     y1, s1 = gpu_scan(lam, V[:, :, :700], hip_device, return_final_state=True)
