@@ -85,6 +85,21 @@ def test_scan_shapes_large_grid(hip_device, kdecay_lib, dname, D):
         assert rel_err(fin, sref) <= 1e-5, f"final state N={N}"
 
 
+@pytest.mark.parametrize("N", [4096, 4097])
+def test_chunk_size_switch(hip_device, kdecay_lib, N):
+    """64 streams of bf16 D=64: N=4096 is exactly 512 chunks of 512 rows (the
+    library takes 256-row chunks), N=4097 is 576 (it keeps 512-row chunks)."""
+    g = torch.Generator().manual_seed(170)
+    lam = lam_uniform(8, 0.5, 0.9999, g)
+    V = torch.randn(8, 8, N, 64, generator=g).to(torch.bfloat16)
+    ws = kdecay_lib.kdecay_scan_workspace_bytes(8, 8, N, 64, 1)
+    assert ws == 256 + 8 * 8 * (16 if N == 4096 else 9) * 64 * 8
+    y, fin = gpu_scan(lam, V, hip_device, return_final_state=True)
+    ref, sref = O.scan(lam, V)
+    assert_parity(y, ref, torch.bfloat16, f"N={N}")
+    assert rel_err(fin, sref) <= 1e-5
+
+
 def test_c1_fp32_full(hip_device, kdecay_lib):
     lam, V = c1_inputs()
     y = gpu_scan(lam, V, hip_device)
