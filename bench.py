@@ -380,15 +380,27 @@ def cpu_extras(torch):
     g = torch.Generator().manual_seed(2)
     S, H, D, steps = 256, 12, 64, 128
     lam = c2_lam(H, torch)
-    state = torch.randn(S, H, D, generator=g)
+    state0 = torch.randn(S, H, D, generator=g)
     vs = torch.randn(steps, S, H, D, generator=g).to(torch.bfloat16)
-    O.step(lam, state, vs[0], 100)
+    O.step(lam, state0, vs[0], 100)
+    state = state0
     t = time.perf_counter()
     for k in range(steps):
         _, state = O.step(lam, state, vs[k], 1000 + k)
     sec = time.perf_counter() - t
+    # The same steps on the GPU from the same start, checked against the
+    # restatement: the new state must be bit-identical after every step.
+    import kilat_amd
+
+    dev = torch.device("cuda", 0)
+    lam_d, st_gpu, st_cpu, same = lam.to(dev), state0.to(dev), state0, 0
+    for k in range(steps):
+        _, st_cpu = O.step(lam, st_cpu, vs[k], 1000 + k)
+        _, st_gpu = kilat_amd.decay_step(lam_d, st_gpu, vs[k].to(dev), 1000 + k)
+        same += int(torch.equal(st_gpu.cpu(), st_cpu))
     out["C3_step"] = {"config": "256 x 12 x 64, bf16 v_t, fp32 state, batch-shared t_pos, 128 steps",
-                      "us_per_step": round(sec / steps * 1e6, 2), "tokens_per_s": round(S * steps / sec, 1)}
+                      "us_per_step": round(sec / steps * 1e6, 2), "tokens_per_s": round(S * steps / sec, 1),
+                      "gpu_state_bitwise_steps": f"{same}/{steps}"}
 
     g = torch.Generator().manual_seed(3)
     V = torch.randn(1, 16, 65536, 128, generator=g).to(torch.bfloat16).float()
