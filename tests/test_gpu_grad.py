@@ -140,6 +140,25 @@ def test_backward_init_final_offset(hip_device, kdecay_lib):
     check(dv, dl, di, rdv, rdl, rdi, torch.float32, "init+gfin+offset")
 
 
+@pytest.mark.parametrize("dname", ["f32", "bf16"])
+def test_backward_init_final_offset_large_grid(hip_device, kdecay_lib, dname):
+    """Carry-in state, final-state gradient and position offset on grids of
+    more than 512 forward chunks at 512 rows (576 bf16, 1152 f32: the 16-row
+    forward kernel) and 2016/4032 backward chunks, against the fp64 adjoint
+    recurrence."""
+    dtype = DTYPES[dname]
+    g = torch.Generator().manual_seed(212)
+    B, H, N, D = 12, 8, 2600, 64
+    lam = lam_uniform(H, 0.8, 0.9999, g)
+    V = torch.randn(B, H, N, D, generator=g).to(dtype)
+    gy = torch.randn(B, H, N, D, generator=g).to(dtype)
+    init = torch.randn(B, H, D, generator=g)
+    gfin = torch.randn(B, H, D, generator=g)
+    dv, dl, di = gpu_grads(lam, V, gy, hip_device, init=init, gfin=gfin, t_offset=33)
+    rdv, rdl, rdi = O.scan_grads_f64(lam, V, gy, init_state=init, gfin=gfin, t_offset=33)
+    check(dv, dl, di, rdv, rdl, rdi, dtype, f"large grid {dname}")
+
+
 def test_backward_c1_shape_and_drop_in(hip_device, kdecay_lib):
     """C1 (B=2 N=1024 H=6 D=64 fp32) through triton_global_decay, as a training step calls it."""
     g = torch.Generator().manual_seed(211)
