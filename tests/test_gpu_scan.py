@@ -85,6 +85,22 @@ def test_scan_shapes_large_grid(hip_device, kdecay_lib, dname, D):
         assert rel_err(fin, sref) <= 1e-5, f"final state N={N}"
 
 
+@pytest.mark.parametrize("dname,out", [("f32", None), ("f16", None), ("bf16", torch.float32)])
+def test_scan_several_rounds(hip_device, kdecay_lib, dname, out):
+    """1152 chunks of 512 rows: more than the device holds at once, so the
+    launch runs in rounds and takes the window-2 kernels of each type."""
+    dtype = DTYPES[dname]
+    g = torch.Generator().manual_seed(180)
+    B = 8 if dtype == torch.float32 else 16  # 128 streams (fp32 splits D=64 in two groups)
+    lam = lam_uniform(8, 0.5, 0.9999, g)
+    V = torch.randn(B, 8, 4100, 64, generator=g).to(dtype)
+    y, fin = gpu_scan(lam, V, hip_device, return_final_state=True, out_dtype=out)
+    ref, sref = O.scan(lam, V, out_dtype=out)
+    assert y.dtype == (out or dtype)
+    assert_parity(y, ref, out or dtype, f"{dname} rounds")
+    assert rel_err(fin, sref) <= 1e-5
+
+
 @pytest.mark.parametrize("N", [4096, 4097])
 def test_chunk_size_switch(hip_device, kdecay_lib, N):
     """64 streams of bf16 D=64: N=4096 is exactly 512 chunks of 512 rows (the
