@@ -101,6 +101,24 @@ def test_scan_several_rounds(hip_device, kdecay_lib, dname, out):
     assert rel_err(fin, sref) <= 1e-5
 
 
+def test_mixed_shapes_share_one_workspace(hip_device, kdecay_lib):
+    """Back-to-back launches of different shapes on one stream reuse one
+    workspace: 256- and 512-row chunks, one round and several, single-chunk
+    streams (no look-back) and a second dtype.  Words left by each launch,
+    in layouts the next one does not share, must never be taken for its own."""
+    g = torch.Generator().manual_seed(190)
+    shapes = [(2, 3, 700, 64, torch.bfloat16), (16, 8, 4100, 64, torch.bfloat16),
+              (4, 4, 300, 64, torch.bfloat16), (8, 8, 4100, 64, torch.float32),
+              (2, 3, 200, 64, torch.bfloat16), (1, 16, 9000, 128, torch.bfloat16)]  # N=200: one chunk
+    for k, (B, H, N, D, dt) in enumerate(shapes * 2):
+        lam = lam_uniform(H, 0.5, 0.9999, g)
+        V = torch.randn(B, H, N, D, generator=g).to(dt)
+        y = gpu_scan(lam, V, hip_device)
+        assert_parity(y, O.global_decay(lam, V), dt, f"launch {k} {(B, H, N, D, dt)}")
+    probe = torch.empty(1, 1, 1, 64, device=hip_device)
+    assert kilat_amd.workspace_error(probe) == 0
+
+
 @pytest.mark.parametrize("N", [4096, 4097])
 def test_chunk_size_switch(hip_device, kdecay_lib, N):
     """64 streams of bf16 D=64: N=4096 is exactly 512 chunks of 512 rows (the
