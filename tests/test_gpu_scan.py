@@ -14,6 +14,7 @@ import torch
 
 import kilat_amd
 from kilat_amd import _lib
+from oracle import c_oracle as C
 from oracle import decay_oracle as O
 from tests.decay_cases import c1_inputs, c2_inputs, c4_inputs, lam_uniform, max_abs, rel_err
 
@@ -99,6 +100,46 @@ def test_scan_several_rounds(hip_device, kdecay_lib, dname, out):
     assert y.dtype == (out or dtype)
     assert_parity(y, ref, out or dtype, f"{dname} rounds")
     assert rel_err(fin, sref) <= 1e-5
+
+
+def test_randomized_shapes(hip_device, kdecay_lib):
+    """A seeded sweep of 48 random cases against the C restatement: dtypes,
+    head dims, batch and head counts on both sides of the small-grid limit,
+    lengths at and around chunk boundaries, decay factors from 0.3 to 0.9999,
+    contiguous V or the projection's (B,N,H*D) view, with or without a carried
+    state and offset.  Outputs are compared after the reference's storage
+    rounding (its zeros_like(V) output has V's dtype)."""
+    rng = np.random.default_rng(2024)
+    for case in range(48):
+        dname = ["f32", "bf16", "f16"][rng.integers(3)]
+        dtype = DTYPES[dname]
+        D = int(rng.choice([16, 32, 64, 128, 256]))
+        L = chunk_rows(dtype, D, int(rng.choice([8, 16])))
+        B, H = int(rng.integers(1, 25)), int(rng.integers(1, 17))
+        N = int(rng.choice([1, 2, int(rng.integers(3, 300)), L - 1, L, L + 1, 2 * L + int(rng.integers(-3, 4)),
+                            int(rng.integers(1, 9)) * L + int(rng.integers(0, 64))]))
+        N = max(1, min(N, 8_000_000 // (B * H * D) or 1))
+        fused = bool(rng.integers(2))
+        carry = bool(rng.integers(2))
+        t_off = int(rng.integers(0, 5000)) if carry else 0
+        print(f"  case {case}: {dname} B={B} H={H} N={N} D={D} fused={fused} carry={carry}", flush=True)
+        g = torch.Generator().manual_seed(case)
+        lam = (0.3 + (0.9999 - 0.3) * torch.rand(H, generator=g)).float()
+        if fused:
+            V = torch.randn(B, N, H, D, generator=g).to(dtype).transpose(1, 2)
+        else:
+            V = torch.randn(B, H, N, D, generator=g).to(dtype)
+        init = torch.randn(B, H, D, generator=g) if carry else None
+        kw = {"return_final_state": True}
+        if carry:
+            kw.update(initial_state=init.to(hip_device), t_offset=t_off)
+        y, fin = kilat_amd.global_decay_scan(lam.to(hip_device), V.to(hip_device), **kw)
+        torch.cuda.synchronize()
+        ref, sref = C.scan_f32(lam.numpy(), V.float().numpy(), None if init is None else init.numpy(), t_off)
+        ref = torch.from_numpy(ref).to(dtype)
+        assert y.dtype == dtype and y.shape == V.shape
+        assert_parity(y.cpu(), ref, dtype, f"case {case}")
+        assert rel_err(fin.cpu(), torch.from_numpy(sref)) <= 1e-5, f"case {case} final state"
 
 
 def test_mixed_shapes_share_one_workspace(hip_device, kdecay_lib):
