@@ -128,6 +128,36 @@ def test_backward_give_up_is_flagged_not_hung(hip_device, kdecay_lib):
     assert torch.equal(dv1, dv0) and torch.equal(dl1, dl0)
 
 
+def test_backward_randomized(hip_device, kdecay_lib):
+    """A seeded sweep of 24 random backward cases against the fp64 adjoint
+    recurrence: dtypes, head dims, grids on both sides of the forward's
+    small-grid limit, lengths around the 128-row backward chunks, decay
+    factors from 0.3 to 0.9999, with or without carry-in, final-state
+    gradient and offset."""
+    import numpy as np
+
+    rng = np.random.default_rng(4048)
+    for case in range(24):
+        dname = ["f32", "bf16", "f16"][rng.integers(3)]
+        dtype = DTYPES[dname]
+        D = int(rng.choice([16, 32, 64, 128, 256]))
+        B, H = int(rng.integers(1, 13)), int(rng.integers(1, 9))
+        N = int(rng.choice([1, 127, 128, 129, int(rng.integers(2, 3000)), 128 * int(rng.integers(2, 20)) + int(rng.integers(-2, 3))]))
+        N = max(1, min(N, 3_000_000 // (B * H * D) or 1))
+        extra = bool(rng.integers(2))
+        print(f"  bwd case {case}: {dname} B={B} H={H} N={N} D={D} extra={extra}", flush=True)
+        g = torch.Generator().manual_seed(500 + case)
+        lam = (0.3 + (0.9999 - 0.3) * torch.rand(H, generator=g)).float()
+        V = torch.randn(B, H, N, D, generator=g).to(dtype)
+        gy = torch.randn(B, H, N, D, generator=g).to(dtype)
+        init = torch.randn(B, H, D, generator=g) if extra else None
+        gfin = torch.randn(B, H, D, generator=g) if extra else None
+        t_off = int(rng.integers(0, 3000)) if extra else 0
+        dv, dl, di = gpu_grads(lam, V, gy, hip_device, init=init, gfin=gfin, t_offset=t_off)
+        rdv, rdl, rdi = O.scan_grads_f64(lam, V, gy, init_state=init, gfin=gfin, t_offset=t_off)
+        check(dv, dl, di, rdv, rdl, rdi if extra else None, dtype, f"case {case}")
+
+
 def test_backward_init_final_offset(hip_device, kdecay_lib):
     g = torch.Generator().manual_seed(210)
     lam = lam_uniform(4, 0.8, 0.9999, g)
