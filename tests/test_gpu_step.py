@@ -61,6 +61,48 @@ def test_step_mixed_positions_in_one_wavefront(hip_device, kdecay_lib):
     assert ulps(out, ro).max() <= 1
 
 
+def test_step_randomized(hip_device, kdecay_lib):
+    """A seeded sweep of 40 random decode steps against the C restatement:
+    v and out dtypes, batch and head counts, head dims including odd ones
+    (the per-element kernel), scalar or per-sequence positions up to 2^20,
+    in place or not.  The state is bit-identical; the output is within one
+    ulp in fp32 (z's power may round one ulp apart) and one rounding of the
+    output dtype otherwise."""
+    rng = np.random.default_rng(77)
+    dts = [torch.float32, torch.bfloat16, torch.float16]
+    for case in range(40):
+        vdt, odt = dts[rng.integers(3)], dts[rng.integers(3)]
+        B, H = int(rng.integers(1, 65)), int(rng.integers(1, 17))
+        D = int(rng.choice([1, 3, 16, 24, 33, 64, 100, 128, 256]))
+        per_seq = bool(rng.integers(2))
+        tps = [int(rng.choice([0, 1, 2, 3, int(rng.integers(4, 70000)), int(rng.integers(0, 1 << 20))])) for _ in range(B)]
+        in_place = bool(rng.integers(2))
+        print(f"  step case {case}: v={vdt} out={odt} B={B} H={H} D={D} per_seq={per_seq} in_place={in_place}", flush=True)
+        g = torch.Generator().manual_seed(900 + case)
+        lam = (0.3 + (0.9999 - 0.3) * torch.rand(H, generator=g)).float()
+        state = torch.randn(B, H, D, generator=g) * 3
+        v = torch.randn(B, H, D, generator=g).to(vdt)
+        t_pos = torch.tensor(tps, dtype=torch.int32) if per_seq else tps[0]
+        st_d = state.to(hip_device)
+        out, ns = kilat_amd.decay_step(lam.to(hip_device), st_d, v.to(hip_device),
+                                       t_pos.to(hip_device) if per_seq else t_pos,
+                                       out_dtype=odt, new_state=st_d if in_place else None)
+        torch.cuda.synchronize()
+        ro, rs = C.step_f32(lam.numpy(), state.numpy(), v.float().numpy(), tps if per_seq else tps[0])
+        assert torch.equal(ns.cpu(), torch.from_numpy(rs)), f"case {case}: state"
+        if odt == torch.float32:
+            assert ulps(out, torch.from_numpy(ro)).max() <= 1, f"case {case}: out"
+        else:
+            # Both sides round an fp32 value once to the output type; the fp32
+            # values are at most 1 ulp apart, so the rounded ones are at most
+            # one step of the output type apart (compared as bit patterns,
+            # which also covers fp16's subnormal outputs).
+            r = torch.from_numpy(ro).to(odt)
+            a16 = out.cpu().view(torch.int16).to(torch.int32)
+            b16 = r.view(torch.int16).to(torch.int32)
+            assert int((a16 - b16).abs().max()) <= 1, f"case {case}: out"
+
+
 def test_c3_decode_128_steps_bitwise_state(hip_device, kdecay_lib):
     lam, lengths, prefixes, v_steps = c3_inputs()
     S, H, D = len(prefixes), lam.numel(), v_steps.shape[-1]
