@@ -194,6 +194,45 @@ def bench_decode(torch, kilat_amd, dev, steps=500):
             "bytes_per_step": nbytes, "GBps_graph": round(nbytes / (us_graph * 1e-6) / 1e9, 1)}
 
 
+def bench_decode_layers(torch, kilat_amd, dev, replays=200):
+    """One token's decay steps through every layer of the C5 model (12 layers x
+    6 heads x 64 channels, bf16 v_t, fp32 state updated in place, positions in
+    device memory advanced inside the graph), captured once as a HIP graph and
+    replayed once per token, for a decode batch of 8 and of 256 sequences."""
+    L, H, D = 12, 6, 64
+    res = {"config": "C5 decode: 12 layers x 6 heads x 64 per token, one HIP graph per token"}
+    for B in (8, 256):
+        g = torch.Generator(device=dev).manual_seed(6)
+        lams = [c2_lam(H, torch).to(dev) for _ in range(L)]
+        st = [torch.randn(B, H, D, generator=g, device=dev) for _ in range(L)]
+        v_in = torch.randn(L, B, H, D, generator=g, device=dev).to(torch.bfloat16)
+        outs = torch.empty(L, B, H, D, device=dev)
+        tpos = torch.randint(1, 2049, (B,), generator=g, device=dev, dtype=torch.int32)
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                for l in range(L):
+                    kilat_amd.decay_step(lams[l], st[l], v_in[l], tpos, out=outs[l], new_state=st[l])
+                tpos.add_(1)
+        torch.cuda.synchronize()
+        for _ in range(10):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(replays):
+            graph.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / replays
+        res[f"B{B}"] = {"us_per_token": round(us, 3), "us_per_layer": round(us / L, 3),
+                        "tokens_per_s": round(B / (us * 1e-6), 1),
+                        "bytes_per_token": L * B * H * D * (4 + 2 + 4 + 4)}
+    return res
+
+
 def bench_long(torch, kilat_amd, dev, steps=20):
     B, H, N, D = 1, 16, 65536, 128
     u = 0.99 + (0.99999 - 0.99) * torch.rand(H, generator=torch.Generator().manual_seed(3), dtype=torch.float64)
@@ -291,7 +330,7 @@ def bench_e2e(torch, dev, iters=5):
     Timed with the reference's glue (two .contiguous() copies around the op) and with
     layout-fused I/O; the decay op's own share is timed with events around its calls."""
     import kilat_amd
-    from kilat_amd.e2e_model import E2EConfig, KilatE2E
+    from tests.e2e_model import E2EConfig, KilatE2E
 
     torch.manual_seed(4)
     cfg = E2EConfig()
@@ -480,6 +519,8 @@ def main() -> int:
         torch.cuda.empty_cache()
         log("decode step C3")
         extras["decode"] = bench_decode(torch, kilat_amd, dev)
+        log("decode token through 12 layers (C5 shape), graph-replayed")
+        extras["decode_layers"] = bench_decode_layers(torch, kilat_amd, dev)
         log("long context C4")
         extras["long_context"] = bench_long(torch, kilat_amd, dev)
         torch.cuda.empty_cache()

@@ -81,9 +81,13 @@ enum {
  *                under stream capture and graph replay), but it must not be
  *                shared by two launches that can run at the same time (use
  *                one per stream).  A non-zero error word (header word 2: a
- *                look-back gave up waiting, and that launch's output is
- *                wrong) stays set until the caller zeroes the workspace.  It
- *                may be NULL when kdecay_scan_workspace_bytes() returns 0.
+ *                look-back gave up waiting) stays set until the caller
+ *                zeroes the workspace.  Outputs that launch could not
+ *                compute (the rows of a chunk whose look-back gave up, and
+ *                any later rows or final state whose carry came through that
+ *                chunk) are written as NaN, never as finite wrong values.
+ *                It may be NULL when
+ *                kdecay_scan_workspace_bytes() returns 0.
  *
  * Requirements of this (vector) path: D in {16,32,64,128,256}; d-stride 1;
  * 16-byte aligned V and out; the other strides multiples of 16 bytes.
@@ -159,7 +163,9 @@ size_t kdecay_scan_saved_states_floats(int64_t B, int64_t H, int64_t N,
  *   d_init       nullable fp32 [B,H,D]
  *   workspace    kdecay_scan_bwd_workspace_bytes() bytes, 256-byte aligned,
  *                zeroed once; same rules as kdecay_scan_fwd's (it may be the
- *                same buffer when large enough)
+ *                same buffer when large enough).  A bounded wait that gives
+ *                up sets the error word and leaves NaN in the gradients it
+ *                could not compute (dV rows, the head's dlam).
  */
 int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides,
                     const void* gy, const int64_t* gy_strides, void* dV,
@@ -208,8 +214,9 @@ const char* kdecay_last_error_string(void);
  * Test hook, no counterpart in the reference: the bounded waits of later
  * launches (chunk look-back, the backward's dlam reduction) give up after
  * `polls` polls instead of about a second's worth, so a test can force the
- * give-up path: the launch still returns, its output is wrong and the
- * workspace's sticky error word is set.  polls <= 0 restores the default.
+ * give-up path: the launch still returns, the outputs it could not compute
+ * are NaN and the workspace's sticky error word is set.  polls <= 0 restores
+ * the default.
  * Process-wide, not thread-safe; returns the previous setting (0: default).
  */
 int kdecay_debug_set_spin_limit(int polls);

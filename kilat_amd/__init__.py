@@ -10,6 +10,7 @@ from .triton_ops import (
     VECTOR_HEAD_DIMS,
     decay_step,
     global_decay_scan,
+    reserve_workspace,
     triton_global_decay,
     workspace_error,
 )
@@ -21,5 +22,6 @@ __all__ = [
     "decay_step",
     "global_decay_scan",
     "workspace_error",
+    "reserve_workspace",
     "VECTOR_HEAD_DIMS",
 ]

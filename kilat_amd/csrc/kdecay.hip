@@ -270,7 +270,12 @@ __device__ __forceinline__ bool fold_window(const u64 (&w)[W], unsigned tag_agg,
 }
 
 // Look-back of wavefront 0 for chunk c (c >= 1): carry[q] = F(c-1) of channel
-// lane + 64q.  Re-reads the window until every channel's fold succeeds.
+// lane + 64q.  Re-reads the window until every channel's fold succeeds.  A
+// look-back that gives up sets the sticky error word and returns a NaN carry
+// for the channels it could not resolve: every output that carry reaches
+// (the chunk's rows, its inclusive word, and through it later chunks and the
+// final state) is NaN, so a caller that checks its outputs for finite values
+// sees the fault, not a plausible wrong number.
 template <int W, int DG, int DQ>
 __device__ void look_back(const u64* base, int c, unsigned tag_agg, unsigned tag_inc, float mL, unsigned* hdr,
                           int spin_limit, float (&carry)[DQ]) {
@@ -295,7 +300,7 @@ __device__ void look_back(const u64* base, int c, unsigned tag_agg, unsigned tag
       __hip_atomic_store(hdr + HDR_ERROR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
       for (int q = 0; q < DQ; ++q)
-        if (!done[q]) carry[q] = 0.0f;
+        if (!done[q]) carry[q] = __builtin_nanf("");
       return;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -1057,9 +1062,9 @@ struct ChunkBwd {
       for (int k = 0; k < K; ++k) {
         if (i0 + lane + 64 * k >= n) continue;
         for (int spin = 0; (unsigned)(w[k] >> 32) != tag; ++spin) {
-          if (spin >= a.spin_limit) {
+          if (spin >= a.spin_limit) {  // give up: flag it, and the head's dlam becomes NaN
             __hip_atomic_store(a.hdr + HDR_ERROR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            w[k] = (u64)tag << 32;
+            w[k] = ((u64)tag << 32) | 0x7fc00000u;
             break;
           }
           __builtin_amdgcn_s_sleep(1);

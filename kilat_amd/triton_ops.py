@@ -36,6 +36,10 @@ VECTOR_HEAD_DIMS = (16, 32, 64, 128, 256)
 # One zero-initialised workspace per (device, stream); the kernels keep it
 # consistent from launch to launch, so it is never cleared again.
 _workspaces: dict = {}
+# Workspaces replaced by a larger one.  A HIP graph captured with a workspace
+# keeps its raw address, so a workspace that was ever handed to a launch is
+# never freed: it stays referenced here for the life of the process.
+_retired: list = []
 
 
 def _require_hip(t: torch.Tensor, name: str) -> None:
@@ -98,14 +102,49 @@ def _fwd_workspace_bytes(lib, B: int, H: int, N: int, D: int, v_code: int) -> in
 
 
 def _workspace(device: torch.device, stream: int, nbytes: int) -> Optional[torch.Tensor]:
+    """The look-back workspace of (device, stream), grown to `nbytes` if needed.
+
+    Growing allocates and zeroes a new buffer, which must not happen inside a
+    stream capture (the buffer would belong to the graph's memory pool and
+    its zeroing would be replayed); that raises instead.  The replaced buffer
+    is kept alive (_retired): graphs captured earlier still write to it.
+    """
     if nbytes == 0:
         return None
     key = (device.index, stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-        _workspaces[key] = ws
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                f"kilat_amd: this launch needs a decay-scan workspace of {nbytes} bytes on the stream being "
+                f"captured, which has {0 if ws is None else ws.numel()}; call kilat_amd.reserve_workspace() "
+                "(or run the largest shape once eagerly) on that stream before capturing"
+            )
+        new = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        if ws is not None:
+            _retired.append(ws)
+        _workspaces[key] = ws = new
     return ws
+
+
+def reserve_workspace(
+    B: int, H: int, N: int, D: int, dtype: torch.dtype = torch.bfloat16,
+    device: Optional[torch.device] = None, backward: bool = True,
+) -> int:
+    """Make the current stream's workspace large enough for scans of this shape
+    (and their backward when `backward`), so that they can be captured into a
+    HIP graph.  Returns the workspace size in bytes."""
+    dev = torch.device("cuda") if device is None else torch.device(device)
+    if dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    code = _dtype_code(torch.empty((), dtype=dtype), "dtype")
+    lib = _lib.load()
+    nbytes = lib.kdecay_scan_workspace_bytes(B, H, N, D, code)
+    if backward:
+        nbytes = max(nbytes, lib.kdecay_scan_bwd_workspace_bytes(B, H, N, D, code))
+    with _on_device(dev):
+        ws = _workspace(dev, _stream_ptr(dev), nbytes)
+    return 0 if ws is None else ws.numel()
 
 
 def workspace_error(V: torch.Tensor, clear: bool = False) -> int:
@@ -404,4 +443,5 @@ def decay_step(
     return out, new_state
 
 
-__all__ = ["triton_global_decay", "decay_step", "global_decay_scan", "workspace_error", "VECTOR_HEAD_DIMS"]
+__all__ = ["triton_global_decay", "decay_step", "global_decay_scan", "workspace_error", "reserve_workspace",
+           "VECTOR_HEAD_DIMS"]

@@ -98,14 +98,6 @@ def seed_state(lam: torch.Tensor, V_global: torch.Tensor, x_dtype: torch.dtype) 
     return acc_state
 
 
-def z_table(lam: torch.Tensor, N: int, t_offset: int = 0) -> torch.Tensor:
-    """[H, N] normalisers, one reference expression per position (triton_ops.py:245)."""
-    H = lam.shape[0]
-    lam_b = lam.view(1, H, 1)
-    cols = [((1.0 - lam_b ** (t_offset + t + 1)) / (1.0 - lam_b + 1e-6)).view(H) for t in range(N)]
-    return torch.stack(cols, 1)
-
-
 def scan_grads_f64(
     lam: torch.Tensor,
     V: torch.Tensor,

@@ -64,6 +64,22 @@ def rel_err(y: torch.Tensor, ref: torch.Tensor) -> float:
     return float((num / den).max())
 
 
+def elementwise_rel(y: torch.Tensor, ref: torch.Tensor, floor: float = 1e-3):
+    """Elementwise |y - ref| / |ref| over the elements with |ref| > floor * max|ref|
+    (fp64): returns (max, 99.99th percentile, elements counted).  Near a zero
+    crossing of y the ratio is dominated by rounding of the partial sums, in
+    the reference's own recurrence as much as in any reassociated one; the
+    floor leaves those elements out."""
+    y = y.double().cpu().reshape(-1)
+    ref = ref.double().cpu().reshape(-1)
+    keep = ref.abs() > floor * float(ref.abs().max())
+    r = ((y - ref).abs() / ref.abs())[keep]
+    if r.numel() == 0:
+        return 0.0, 0.0, 0
+    q = float(torch.quantile(r, 0.9999)) if r.numel() <= 1 << 24 else float(r.sort().values[int(0.9999 * (r.numel() - 1))])
+    return float(r.max()), q, int(r.numel())
+
+
 def max_abs(y: torch.Tensor, ref: torch.Tensor) -> float:
     return float((y.double().cpu() - ref.double().cpu()).abs().max())
 

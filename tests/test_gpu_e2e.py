@@ -1,4 +1,4 @@
-"""End-to-end: the KilatTransformer forward restatement (kilat_amd.e2e_model) with
+"""End-to-end: the KilatTransformer forward restatement (tests/e2e_model.py) with
 the decay path on the HIP kernel matches the same model on the CPU with the
 oracle's decay (the reference's _cpu_global_decay, triton_ops.py:232-247), on
 identical weights and tokens.  Tolerance: logits within 1e-4 relative to their
@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import kilat_amd
-from kilat_amd.e2e_model import E2EConfig, KilatE2E
+from tests.e2e_model import E2EConfig, KilatE2E
 from oracle import decay_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -73,3 +73,48 @@ def test_e2e_training_gradients_match_cpu_reference_decay(hip_device, kdecay_lib
         gpu = grads[n].grad.cpu()
         err = float((gpu - r).abs().max() / r.abs().max().clamp_min(1e-30))
         assert err <= 1e-3, f"{n}: grad rel err {err:.3e}"
+
+
+def test_c5_full_config_every_layer_matches_oracle(hip_device, kdecay_lib):
+    """The C5 configuration itself: n_embd 768, 12 layers, 12 heads with
+    recall_ratio 0.5 (6 decay heads of 64 channels per layer), MoE 8 x top-2
+    (+2 shared), vocab 50000, random init, bf16 autocast, B=8 N=1024.  The
+    decay op is wrapped to record each layer's (lam, V, y) on the GPU; every
+    one of the 12 outputs is checked against the oracle's decay
+    (triton_ops.py:232-247) on the same lam and V, to the bf16 tolerance
+    (max-abs <= 2e-2), with the reference's glue copies and with the
+    layout-fused view (attention.py:319-374)."""
+    torch.manual_seed(4)
+    cfg = E2EConfig()
+    calls = []
+
+    def recording_decay(lam, V):
+        y = kilat_amd.triton_global_decay(lam, V)
+        calls.append((lam.detach().cpu(), V.detach().cpu(), y.detach().cpu()))
+        return y
+
+    model = KilatE2E(cfg, recording_decay).to(hip_device).eval()
+    with torch.no_grad():  # a spread of decay rates, up to 0.9999, per head and layer
+        for blk in model.layers:
+            u = 0.5 + (0.9999 - 0.5) * torch.rand(blk.attn.n_global, dtype=torch.float64)
+            blk.attn.log_lambda.copy_(torch.log(u / (1 - u)).float())
+    ids = torch.randint(0, cfg.vocab_size, (8, 1024), generator=torch.Generator().manual_seed(44)).to(hip_device)
+    logits = {}
+    for fused in (False, True):
+        calls.clear()
+        model.set_decay(recording_decay, fused_layout=fused)
+        print(f"  C5 forward fused_layout={fused}", flush=True)
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            lg, _ = model(ids)
+        torch.cuda.synchronize()
+        logits[fused] = lg.float().cpu()
+        assert bool(torch.isfinite(logits[fused]).all())
+        assert len(calls) == cfg.n_layer
+        for layer, (lam, V, y) in enumerate(calls):
+            assert V.shape == (8, 6, 1024, 64) and V.dtype == torch.bfloat16 and y.dtype == torch.bfloat16
+            ref = O.global_decay(lam, V)
+            err = float((y.double() - ref.double()).abs().max())
+            print(f"    layer {layer}: max_abs {err:.3e}", flush=True)
+            assert err <= 2e-2, f"fused={fused} layer {layer}: max_abs {err:.3e}"
+    # the two layouts feed the decay op the same values and get the same bits back
+    assert torch.equal(logits[False], logits[True])

@@ -100,8 +100,9 @@ def test_backward_give_up_is_flagged_not_hung(hip_device, kdecay_lib):
     """Force the backward's bounded waits (the reverse look-back and the wait
     for a head's dlam partials) to give up after one poll, through the
     library's test hook: every launch still returns and sets the workspace's
-    sticky error word, and once the hook and the word are cleared the same
-    workspace gives gradients bit-identical to the first run."""
+    sticky error word, the launch that gives up leaves NaN in the gradients
+    it could not compute, and once the hook and the word are cleared the same
+    workspace gives finite gradients bit-identical to the first run."""
     from kilat_amd.triton_ops import _stream_ptr, _workspaces
 
     g = torch.Generator().manual_seed(43)
@@ -115,10 +116,18 @@ def test_backward_give_up_is_flagged_not_hung(hip_device, kdecay_lib):
         probe = V[:, :, :1].to(hip_device)  # selects the workspace of this device and stream
         assert kilat_amd.workspace_error(probe) == 0
         kdecay_lib.kdecay_debug_set_spin_limit(1)
+        flagged = []
         try:
             for k in range(3):
                 print(f"  forced give-up backward {k}", flush=True)
-                gpu_grads(lam, V, gy, hip_device)
+                dv, dl, _ = gpu_grads(lam, V, gy, hip_device)
+                torch.cuda.synchronize()
+                nan = bool(torch.isnan(dv).any()) or bool(torch.isnan(dl).any())
+                err = kilat_amd.workspace_error(probe)
+                # the launch that first sets the sticky word leaves NaN in what it could not compute
+                if err and not flagged:
+                    assert nan, f"launch {k} gave up but its gradients are all finite"
+                flagged.append(err)
         finally:
             kdecay_lib.kdecay_debug_set_spin_limit(0)
         assert kilat_amd.workspace_error(probe) == 1
@@ -126,6 +135,7 @@ def test_backward_give_up_is_flagged_not_hung(hip_device, kdecay_lib):
         dv1, dl1, _ = gpu_grads(lam, V, gy, hip_device)
         assert kilat_amd.workspace_error(probe) == 0
     assert torch.equal(dv1, dv0) and torch.equal(dl1, dl0)
+    assert bool(torch.isfinite(dv1).all()) and bool(torch.isfinite(dl1).all())
 
 
 def test_backward_randomized(hip_device, kdecay_lib):

@@ -16,7 +16,7 @@ import kilat_amd
 from kilat_amd import _lib
 from oracle import c_oracle as C
 from oracle import decay_oracle as O
-from tests.decay_cases import c1_inputs, c2_inputs, c4_inputs, lam_uniform, max_abs, rel_err
+from tests.decay_cases import c1_inputs, c2_inputs, c4_inputs, elementwise_rel, lam_uniform, max_abs, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -176,10 +176,23 @@ def test_chunk_size_switch(hip_device, kdecay_lib, N):
 
 
 def test_c1_fp32_full(hip_device, kdecay_lib):
+    """C1 to the fp32 tolerance, read normwise per stream (max|y-ref| / max|ref|
+    <= 1e-5, the gate).  The elementwise ratio |y-ref|/|ref| over elements
+    with |ref| > 1e-3 max|ref| is reported beside it, with its own bound."""
     lam, V = c1_inputs()
     y = gpu_scan(lam, V, hip_device)
     ref = O.global_decay(lam, V)
     assert_parity(y, ref, torch.float32, "C1")
+    emax, e9999, n = elementwise_rel(y, ref)
+    # The same figures for the reference's own fp32 recurrence against exact
+    # (fp64) arithmetic on the same inputs: the scale elementwise error has
+    # in fp32 at all (2.3e-5 max, 1.1e-5 at the 99.99th percentile here).
+    y64 = O.global_decay(lam.double(), V.double())
+    rmax, r9999, _ = elementwise_rel(ref, y64)
+    print(f"  C1 fp32 vs oracle: normwise {rel_err(y, ref):.3e}; elementwise over {n} elements: "
+          f"max {emax:.3e}, 99.99th percentile {e9999:.3e}  (oracle vs fp64: max {rmax:.3e}, "
+          f"99.99th {r9999:.3e})", flush=True)
+    assert emax <= 1e-4 and e9999 <= 5e-5, (emax, e9999)
 
 
 def test_c2_bf16_full(hip_device, kdecay_lib):
@@ -366,9 +379,9 @@ def test_workspace_clean_after_suite(hip_device, kdecay_lib):
 def test_lookback_give_up_is_flagged_not_hung(hip_device, kdecay_lib):
     """Force the bounded look-back waits to give up after two polls
     (kdecay_debug_set_spin_limit, the library's test hook): every launch still
-    returns and sets the workspace's sticky error word, and once the hook and
-    the word are cleared the same workspace serves a normal launch
-    bit-identical to the first."""
+    returns and sets the workspace's sticky error word, the launch that gives
+    up writes NaN in the rows whose carry it could not compute, and once the hook and the word are cleared the same workspace
+    serves a normal launch bit-identical to the first."""
     from kilat_amd.triton_ops import _stream_ptr, _workspaces
 
     g = torch.Generator().manual_seed(41)
@@ -381,11 +394,18 @@ def test_lookback_give_up_is_flagged_not_hung(hip_device, kdecay_lib):
         torch.cuda.synchronize()
         assert kilat_amd.workspace_error(V) == 0
         kdecay_lib.kdecay_debug_set_spin_limit(1)
+        flagged = False
         try:
             for k in range(3):
                 print(f"  forced give-up launch {k}", flush=True)
-                kilat_amd.global_decay_scan(lam, V)
-            torch.cuda.synchronize()
+                y, fin = kilat_amd.global_decay_scan(lam, V, return_final_state=True)
+                torch.cuda.synchronize()
+                err = kilat_amd.workspace_error(V)
+                if err and not flagged:  # the launch that gave up: NaN, not finite wrong values
+                    assert bool(torch.isnan(y).any()), k
+                    flagged = True
+                if not err:
+                    assert bool(torch.isfinite(y).all()), k
         finally:
             kdecay_lib.kdecay_debug_set_spin_limit(0)
         assert kilat_amd.workspace_error(V) == 1
@@ -393,7 +413,7 @@ def test_lookback_give_up_is_flagged_not_hung(hip_device, kdecay_lib):
         y = kilat_amd.global_decay_scan(lam, V)
         torch.cuda.synchronize()
         assert kilat_amd.workspace_error(V) == 0
-    assert torch.equal(y, y_ref)
+    assert torch.equal(y, y_ref) and bool(torch.isfinite(y).all())
 
 
 def test_integration_ctypes_stub_matches_package(hip_device, kdecay_lib):
@@ -454,8 +474,8 @@ def test_native_c_abi_caller(hip_device, kdecay_lib):
 
     from tests import c_abi_build
 
-    if not os.path.exists(c_abi_build.BINARY):
-        pytest.skip("tests/_build/c_abi_check is not built (run __graft_entry__.build())")
+    assert os.path.exists(c_abi_build.BINARY), (
+        "tests/_build/c_abi_check is missing: __graft_entry__.build() builds it next to libkdecay.so")
     print("  running tests/_build/c_abi_check", flush=True)
     r = subprocess.run([c_abi_build.BINARY], capture_output=True, text=True, timeout=60)
     print(r.stdout.strip(), flush=True)

@@ -248,6 +248,16 @@ def test_graph_capture_scan_and_step_replays(hip_device, kdecay_lib):
             o.copy_(o2)
             ns.copy_(ns2)
     torch.cuda.synchronize()
+    # The eager results the replays are compared with, against the oracle:
+    # the scan to the bf16 tolerance, the step's state bit for bit and its
+    # output within one ulp (the double-precision power inside z).
+    lam_c = lam.cpu()
+    ref, sref = O.scan(lam_c, V.cpu())
+    assert float((y_ref.cpu().double() - ref.double()).abs().max()) <= 2e-2
+    assert float(((fin_ref.cpu() - sref).abs().max() / sref.abs().max())) <= 1e-5
+    ro, rs = O.step(lam_c, fin_ref.cpu(), v.cpu(), 3000)
+    assert torch.equal(ns_ref.cpu(), rs)
+    assert ulps(o_ref, ro).max() <= 1
     for r in range(4):
         print(f"  graph replay {r}", flush=True)
         y.zero_(); o.zero_(); ns.zero_()
@@ -261,3 +271,124 @@ def test_graph_capture_scan_and_step_replays(hip_device, kdecay_lib):
         torch.cuda.synchronize()
         assert torch.equal(ye, y_ref)
     assert kilat_amd.workspace_error(V) == 0
+
+
+def fresh_workspace_stream(dev):
+    """A side stream with no workspace yet.  torch hands out streams from a
+    small pool, so an earlier test may have used this one: its workspace is
+    retired (kept alive, as the shim does) rather than reused."""
+    from kilat_amd import triton_ops
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    old = triton_ops._workspaces.pop((dev.index, stream.cuda_stream), None)
+    if old is not None:
+        triton_ops._retired.append(old)
+    return stream
+
+
+def test_graph_survives_workspace_growth(hip_device, kdecay_lib):
+    """A graph captured with the stream's workspace keeps writing to that
+    buffer: a later eager scan that needs a larger workspace on the same
+    stream must not free it.  Capture, grow the workspace with a longer eager
+    scan, let the allocator hand out fresh blocks, then replay and check the
+    replay against the oracle."""
+    from kilat_amd import triton_ops
+
+    g = torch.Generator().manual_seed(25)
+    lam = lam_uniform(4, 0.5, 0.999, g)
+    V = torch.randn(2, 4, 3000, 64, generator=g).to(torch.bfloat16)
+    Vd, lamd = V.to(hip_device), lam.to(hip_device)
+    stream = fresh_workspace_stream(hip_device)
+    with torch.cuda.stream(stream):
+        kilat_amd.global_decay_scan(lamd, Vd)  # workspace sized for N=3000
+        y = torch.empty_like(Vd)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            y.copy_(kilat_amd.global_decay_scan(lamd, Vd))
+        key = (hip_device.index, stream.cuda_stream)
+        captured = triton_ops._workspaces[key].data_ptr()
+        # 40000 rows need a larger workspace: the captured one is replaced
+        Vl = torch.randn(2, 4, 40000, 64, generator=g).to(torch.bfloat16)
+        yl = kilat_amd.global_decay_scan(lamd, Vl.to(hip_device))
+        assert triton_ops._workspaces[key].data_ptr() != captured
+        assert any(w.data_ptr() == captured for w in triton_ops._retired)
+        filler = [torch.full((1 << 20,), 7, dtype=torch.uint8, device=hip_device) for _ in range(8)]
+    torch.cuda.synchronize()
+    ref = O.global_decay(lam, V)
+    assert float((yl.cpu().double() - O.global_decay(lam, Vl).double()).abs().max()) <= 2e-2
+    for r in range(3):
+        print(f"  replay after growth {r}", flush=True)
+        y.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert float((y.cpu().double() - ref.double()).abs().max()) <= 2e-2, r
+    assert all(int(f[0]) == 7 and int(f[-1]) == 7 for f in filler)
+
+
+def test_workspace_growth_inside_capture_raises(hip_device, kdecay_lib):
+    """A shape first seen inside a stream capture would need a new workspace
+    there: the shim raises with advice instead of allocating in the capture;
+    after reserve_workspace the same capture succeeds."""
+    g = torch.Generator().manual_seed(26)
+    lam = lam_uniform(3, 0.5, 0.999, g).to(hip_device)
+    V = torch.randn(2, 3, 5000, 64, generator=g).to(torch.bfloat16).to(hip_device)
+    stream = fresh_workspace_stream(hip_device)
+    with torch.cuda.stream(stream):
+        graph = torch.cuda.CUDAGraph()
+        with pytest.raises(RuntimeError, match="reserve_workspace"):
+            with torch.cuda.graph(graph, stream=stream):
+                kilat_amd.global_decay_scan(lam, V)
+        assert kilat_amd.reserve_workspace(2, 3, 5000, 64, torch.bfloat16) > 0
+        y = torch.empty_like(V)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            y.copy_(kilat_amd.global_decay_scan(lam, V))
+    torch.cuda.synchronize()
+    ref = O.global_decay(lam.cpu(), V.cpu())
+    for r in range(2):
+        y.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert float((y.cpu().double() - ref.double()).abs().max()) <= 2e-2, r
+
+
+@pytest.mark.parametrize("B", [8, 256])
+def test_decode_token_all_layers_in_one_graph(hip_device, kdecay_lib, B):
+    """One token's decay work through every layer of the C5 model (12 layers
+    x 6 heads x 64 channels), captured once in a HIP graph and replayed per
+    token, as the reference's decode loop runs one model forward per token
+    (generation_mixin.py:484-509) with each layer's inline update
+    (attention.py:344-360).  The positions live in device memory and advance
+    inside the graph.  Every layer's state after every token is checked bit
+    for bit against the oracle's step, and its output within one ulp."""
+    L, H, D, T = 12, 6, 64, 6
+    g = torch.Generator().manual_seed(27 + B)
+    lams = [lam_uniform(H, 0.5, 0.9999, g) for _ in range(L)]
+    states = [torch.randn(B, H, D, generator=g) for _ in range(L)]
+    vs = torch.randn(T, L, B, H, D, generator=g).to(torch.bfloat16)
+    tpos0 = torch.randint(1, 2049, (B,), generator=g, dtype=torch.int32)
+    lam_d = [l.to(hip_device) for l in lams]
+    st_d = [s.to(hip_device) for s in states]
+    v_in = torch.empty(L, B, H, D, dtype=torch.bfloat16, device=hip_device)
+    outs = torch.empty(L, B, H, D, device=hip_device)
+    tpos = tpos0.to(hip_device)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for l in range(L):
+                kilat_amd.decay_step(lam_d[l], st_d[l], v_in[l], tpos, out=outs[l], new_state=st_d[l])
+            tpos.add_(1)
+    torch.cuda.synchronize()
+    ref_states = [s.clone() for s in states]
+    for t in range(T):
+        v_in.copy_(vs[t].to(hip_device))
+        graph.replay()
+        torch.cuda.synchronize()
+        for l in range(L):
+            ro, ref_states[l] = O.step(lams[l], ref_states[l], vs[t, l], (tpos0 + t).tolist())
+            assert torch.equal(st_d[l].cpu(), ref_states[l]), (t, l)
+            assert ulps(outs[l], ro).max() <= 1, (t, l)
+    assert torch.equal(tpos.cpu(), tpos0 + T)

@@ -334,7 +334,7 @@ def test_adjoint_grads_match_autograd(case):
 
 def test_e2e_model_runs_on_cpu_with_oracle_decay():
     """Host-side check of the end-to-end restatement (shapes, tied head, finite loss)."""
-    from kilat_amd.e2e_model import E2EConfig, KilatE2E
+    from tests.e2e_model import E2EConfig, KilatE2E
 
     torch.manual_seed(42)
     cfg = E2EConfig(vocab_size=128, n_embd=32, n_layer=2, n_head=4, num_experts=4, active_experts=2)
