@@ -104,6 +104,42 @@ int kdecay_scan_fwd(const void* V, int v_dtype, const int64_t* v_strides,
 size_t kdecay_scan_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D,
                                    int v_dtype);
 
+/* Size of the fixed device array kdecay_scan_fwd_noalloc uses as workspace. */
+#define KDECAY_NOALLOC_WORKSPACE_BYTES ((size_t)8 << 20)
+
+/*
+ * Full-sequence scan that allocates nothing: kdecay_scan_fwd with the same
+ * kernels and the same results, but its look-back workspace is a fixed array
+ * of KDECAY_NOALLOC_WORKSPACE_BYTES (8 MiB) in the library's own device
+ * memory, one per GPU, held until the process ends.
+ * No counterpart in the reference.  It is for callers that cannot allocate
+ * device memory or own a workspace: code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  The caller still passes
+ * V, out, lam and the optional states; no hipMalloc, hipFree or other
+ * allocating call is made.
+ *   - Shapes whose kdecay_scan_workspace_bytes() exceeds
+ *     KDECAY_NOALLOC_WORKSPACE_BYTES (about 16K chunks: 1 GiB of bf16 V) are
+ *     rejected with KDECAY_EWORKSPACE before anything is launched.
+ *   - The first call on a GPU looks the array up and enqueues its one-time
+ *     clear (a fill kernel) on `stream`, ahead of the scan.
+ *   - Every call on one GPU in a process shares that GPU's array (each
+ *     process has its own): calls that can overlap on one GPU (two streams,
+ *     two threads) race and give wrong results; serialise them, e.g. on one
+ *     stream.  The array keeps the last call's contents (launch epoch and
+ *     look-back words), which the next call needs no clearing for.
+ *   - A look-back give-up leaves NaN in the outputs it could not compute, as
+ *     kdecay_scan_fwd does; the sticky error word lives in the array and is
+ *     not readable through this API.
+ * Every other argument as kdecay_scan_fwd.
+ */
+int kdecay_scan_fwd_noalloc(const void* V, int v_dtype,
+                            const int64_t* v_strides, void* out,
+                            int out_dtype, const int64_t* out_strides,
+                            const float* lam, const float* init_state,
+                            float* final_state, int64_t B, int64_t H,
+                            int64_t N, int64_t D, int64_t t_offset,
+                            void* stream);
+
 /*
  * Straight sequential scan: one lane per (b,h,d) column walks all N
  * positions.  Same arguments and results as kdecay_scan_fwd (any strides, any

@@ -25,10 +25,13 @@ KDECAY_ESHAPE = -3
 KDECAY_ELAYOUT = -4
 KDECAY_EWORKSPACE = -5
 
+KDECAY_NOALLOC_WORKSPACE_BYTES = 8 << 20  # include/kdecay.h
+
 # Every symbol include/kdecay.h declares.
 EXPORTS = (
     "kdecay_scan_fwd",
     "kdecay_scan_workspace_bytes",
+    "kdecay_scan_fwd_noalloc",
     "kdecay_scan_fwd_train",
     "kdecay_scan_saved_states_floats",
     "kdecay_scan_bwd",
@@ -70,6 +73,15 @@ def load() -> ctypes.CDLL:
     ]
     lib.kdecay_scan_workspace_bytes.restype = ctypes.c_size_t
     lib.kdecay_scan_workspace_bytes.argtypes = [_c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int]
+    lib.kdecay_scan_fwd_noalloc.restype = ctypes.c_int
+    lib.kdecay_scan_fwd_noalloc.argtypes = [
+        _c_ptr, ctypes.c_int, _c_i64p,      # V, v_dtype, v_strides
+        _c_ptr, ctypes.c_int, _c_i64p,      # out, out_dtype, out_strides
+        _c_ptr, _c_ptr, _c_ptr,             # lam, init_state, final_state
+        _c_i64, _c_i64, _c_i64, _c_i64,     # B, H, N, D
+        _c_i64,                             # t_offset
+        _c_ptr,                             # stream
+    ]
     lib.kdecay_scan_fwd_train.restype = ctypes.c_int
     lib.kdecay_scan_fwd_train.argtypes = [
         _c_ptr, ctypes.c_int, _c_i64p,      # V, v_dtype, v_strides

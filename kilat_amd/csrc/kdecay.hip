@@ -24,6 +24,7 @@
 #include <hip/hip_runtime.h>
 
 #include <math.h>
+#include <mutex>
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -1226,6 +1227,10 @@ __global__ __launch_bounds__(256) void decay_step4(StepArgs a) {
   store4<TO>(static_cast<TO*>(a.out) + idx, o);
 }
 
+__global__ __launch_bounds__(256) void zero_words(unsigned long long* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = 0ull;
+}
+
 __global__ __launch_bounds__(256) void zero_floats(float* p, int64_t n) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx < n) p[idx] = 0.0f;
@@ -1454,6 +1459,49 @@ int empty_final_state(const float* init, float* fin, int64_t n, hipStream_t s) {
 
 }  // namespace kd
 
+// Look-back workspace of kdecay_scan_fwd_noalloc: a fixed array in the code
+// object's device memory, so that entry point allocates nothing.  Each GPU the
+// library is loaded on holds its own copy, at its own address, until the
+// process ends.  On the host this name is only a stand-in for the symbol, not
+// a device address: host code uses the address hipGetSymbolAddress returns
+// for the current device (scratch_of_current_device), never `scratch` itself.
+static __device__ __align__(256) unsigned char scratch[KDECAY_NOALLOC_WORKSPACE_BYTES];
+
+namespace kd {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device (null until set up)
+
+// Device address of the current device's scratch array.  The first call on a
+// device looks the address up (hipGetSymbolAddress, with that device current)
+// and clears the array once with a fill kernel on `s`, ahead of the caller's
+// launch (a kernel rather than hipMemsetAsync, so that a first call under
+// stream capture records a kernel node; replaying that clear is harmless).
+// Later calls find the epoch protocol's state in place.
+int scratch_of_current_device(hipStream_t s, void** p) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail((int)e, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(KDECAY_EINVAL, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return fail((int)e, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    if (!ptr) return fail(KDECAY_EINVAL, "hipGetSymbolAddress(scratch) returned a null address");
+    hipLaunchKernelGGL(zero_words, dim3(1024), dim3(256), 0, s, static_cast<u64*>(ptr),
+                       (int64_t)(KDECAY_NOALLOC_WORKSPACE_BYTES / sizeof(u64)));
+    const int rc = hip_check("scratch clear launch");
+    if (rc) return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *p = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace kd
+
 using namespace kd;
 
 extern "C" {
@@ -1552,6 +1600,27 @@ int kdecay_scan_fwd(const void* V, int v_dtype, const int64_t* v_strides, void* 
                     void* workspace, size_t workspace_bytes, void* stream) {
   return scan_fwd_impl(V, v_dtype, v_strides, out, out_dtype, out_strides, lam, init_state, final_state, B, H, N, D,
                        t_offset, workspace, workspace_bytes, nullptr, stream);
+}
+
+int kdecay_scan_fwd_noalloc(const void* V, int v_dtype, const int64_t* v_strides, void* out, int out_dtype,
+                            const int64_t* out_strides, const float* lam, const float* init_state,
+                            float* final_state, int64_t B, int64_t H, int64_t N, int64_t D, int64_t t_offset,
+                            void* stream) {
+  const int rc = check_scan_args(V, v_dtype, v_strides, out, out_dtype, out_strides, lam, B, H, N, D);
+  if (rc) return rc;
+  const size_t need = kdecay_scan_workspace_bytes(B, H, N, D, v_dtype);
+  if (need > KDECAY_NOALLOC_WORKSPACE_BYTES)
+    return fail(KDECAY_EWORKSPACE,
+                "kdecay_scan_fwd_noalloc: this shape needs %zu bytes of look-back workspace, more than the "
+                "library's fixed %zu-byte device array; use kdecay_scan_fwd with a workspace",
+                need, (size_t)KDECAY_NOALLOC_WORKSPACE_BYTES);
+  void* ws = nullptr;
+  if (need) {
+    const int e = scratch_of_current_device(static_cast<hipStream_t>(stream), &ws);
+    if (e) return e;
+  }
+  return scan_fwd_impl(V, v_dtype, v_strides, out, out_dtype, out_strides, lam, init_state, final_state, B, H, N, D,
+                       t_offset, ws, need ? (size_t)KDECAY_NOALLOC_WORKSPACE_BYTES : 0, nullptr, stream);
 }
 
 size_t kdecay_scan_saved_states_floats(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {

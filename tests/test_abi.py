@@ -102,6 +102,31 @@ def test_scan_rejects_bad_arguments(kdecay_lib):
     assert rc == _lib.KDECAY_EINVAL
 
 
+def test_noalloc_scan_rejects_oversized_and_bad_arguments(kdecay_lib):
+    """The allocation-free entry point checks its arguments, and that the
+    shape's workspace fits its fixed device array, before it touches the
+    device: a shape needing more than KDECAY_NOALLOC_WORKSPACE_BYTES is
+    refused with KDECAY_EWORKSPACE and a message naming the limit."""
+    lib = kdecay_lib
+    cap = _lib.KDECAY_NOALLOC_WORKSPACE_BYTES
+    B, H, D = 64, 32, 64
+    N = 40 * 512  # 2048 streams x 40 chunks of 512 bf16 rows
+    need = lib.kdecay_scan_workspace_bytes(B, H, N, D, _lib.KDECAY_BF16)
+    assert need > cap
+    st = _lib.strides4((H * N * D, N * D, D, 1))
+    rc = lib.kdecay_scan_fwd_noalloc(FAKE, _lib.KDECAY_BF16, st, FAKE, _lib.KDECAY_BF16, st, FAKE, None, None,
+                                     B, H, N, D, 0, None)
+    assert rc == _lib.KDECAY_EWORKSPACE
+    msg = lib.kdecay_last_error_string().decode()
+    assert str(need) in msg and str(cap) in msg
+    assert lib.kdecay_scan_fwd_noalloc(FAKE, 7, st, FAKE, 7, st, FAKE, None, None, 1, 1, 1, 64, 0,
+                                       None) == _lib.KDECAY_EDTYPE
+    assert lib.kdecay_scan_fwd_noalloc(None, 0, st, FAKE, 0, st, FAKE, None, None, 1, 1, 1, 64, 0,
+                                       None) == _lib.KDECAY_EINVAL
+    # the largest C4-like shape fits: 1 x 16 x 65536 x 128 bf16 needs 2 MiB
+    assert lib.kdecay_scan_workspace_bytes(1, 16, 65536, 128, _lib.KDECAY_BF16) <= cap
+
+
 def test_sequential_and_step_reject_bad_arguments(kdecay_lib):
     lib = kdecay_lib
     s4 = _lib.strides4((1, 1, 1, 1))
