@@ -13,7 +13,8 @@ _kd.kdecay_scan_workspace_bytes.restype = ctypes.c_size_t
 _kd.kdecay_scan_workspace_bytes.argtypes = [_I64, _I64, _I64, _I64, _I]
 _kd.kdecay_last_error_string.restype = ctypes.c_char_p
 _CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
-_WS = {}  # one zeroed workspace per (device, stream), kept for the process
+_WS = {}    # one zeroed workspace per (device, stream)
+_KEEP = []  # replaced workspaces: a captured graph may still use one, so none is ever freed
 
 def _hip_global_decay(lam_scores, V):          # V: [B,H,N,D] on a HIP device, d-stride 1
     B, H, N, D = V.shape
@@ -23,6 +24,7 @@ def _hip_global_decay(lam_scores, V):          # V: [B,H,N,D] on a HIP device, d
     nbytes = _kd.kdecay_scan_workspace_bytes(B, H, N, D, _CODE[V.dtype])
     ws = _WS.get((V.device.index, stream))
     if nbytes and (ws is None or ws.numel() < nbytes):
+        _KEEP.append(ws)
         ws = _WS[(V.device.index, stream)] = torch.zeros(nbytes, dtype=torch.uint8, device=V.device)
     st = lambda t: (ctypes.c_int64 * 4)(*t.stride())
     rc = _kd.kdecay_scan_fwd(V.data_ptr(), _CODE[V.dtype], st(V), out.data_ptr(), _CODE[V.dtype], st(out),
