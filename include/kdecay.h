@@ -89,8 +89,9 @@ enum {
  *                It may be NULL when
  *                kdecay_scan_workspace_bytes() returns 0.
  *
- * Requirements of this (vector) path: D in {16,32,64,128,256}; d-stride 1;
- * 16-byte aligned V and out; the other strides multiples of 16 bytes.
+ * Requirements of this (vector) path: D = 16, 32, or a multiple of 64 (bf16,
+ * fp16) or 32 (fp32) channels; d-stride 1; 16-byte aligned V and out; the
+ * other strides multiples of 16 bytes.
  * Anything else returns KDECAY_ELAYOUT / KDECAY_ESHAPE without launching.
  */
 int kdecay_scan_fwd(const void* V, int v_dtype, const int64_t* v_strides,

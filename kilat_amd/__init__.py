@@ -7,7 +7,7 @@ kilat/arc/attention.py:344-360), as hand-written HIP kernels in libkdecay.so
 behind a C ABI (include/kdecay.h).
 """
 from .triton_ops import (
-    VECTOR_HEAD_DIMS,
+    chunked_head_dim,
     decay_step,
     global_decay_scan,
     reserve_workspace,
@@ -23,5 +23,5 @@ __all__ = [
     "global_decay_scan",
     "workspace_error",
     "reserve_workspace",
-    "VECTOR_HEAD_DIMS",
+    "chunked_head_dim",
 ]

@@ -1342,10 +1342,13 @@ int rows_per_lane(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   return (N + L - 1) / L * nstream <= kSmallGrid ? kRSmall : kR;
 }
 
+// Head dims of the chunked kernels: 16, 32, or any multiple of a full
+// 128-byte channel group (64 bf16/fp16 or 32 fp32 channels); a head is then
+// D / group_width independent streams.  (A group of 16 or 32 channels takes
+// 2 or 4 lanes per row; other widths would not divide a wavefront.)
 bool head_dim_ok(int v_dtype, int64_t D) {
-  if (!(D == 16 || D == 32 || D == 64 || D == 128 || D == 256)) return false;
-  const int64_t vw = 16 / elem_size(v_dtype);
-  return group_width(v_dtype, D) >= vw && D % group_width(v_dtype, D) == 0;
+  const int64_t full = 128 / elem_size(v_dtype);
+  return D == 16 || D == 32 || (D > 0 && D % full == 0);
 }
 
 template <typename TI, typename TO, int DG, int R = kR, int NW = kNW, int WPE = kWPE>
@@ -1534,7 +1537,8 @@ static int scan_fwd_impl(const void* V, int v_dtype, const int64_t* v_strides, v
   if (B * H * D == 0) return 0;
   if (N == 0) return empty_final_state(init_state, final_state, B * H * D, s);
   if (!head_dim_ok(v_dtype, D))
-    return fail(KDECAY_ESHAPE, "head dim D=%lld not in {16,32,64,128,256}", (long long)D);
+    return fail(KDECAY_ESHAPE, "head dim D=%lld is not 16, 32 or a multiple of %d", (long long)D,
+                128 / elem_size(v_dtype));
 
   const int64_t vw_in = 16 / elem_size(v_dtype);
   const int64_t vw_out = 16 / elem_size(out_dtype);
@@ -1673,7 +1677,8 @@ int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides, const 
   }
   if (!V || !gy || !dV || !v_strides || !gy_strides || !dv_strides) return fail(KDECAY_EINVAL, "null pointer argument");
   if (!head_dim_ok(v_dtype, D))
-    return fail(KDECAY_ESHAPE, "head dim D=%lld not in {16,32,64,128,256}", (long long)D);
+    return fail(KDECAY_ESHAPE, "head dim D=%lld is not 16, 32 or a multiple of %d", (long long)D,
+                128 / elem_size(v_dtype));
   const int64_t vw = 16 / elem_size(v_dtype);
   if (v_strides[3] != 1 || gy_strides[3] != 1 || dv_strides[3] != 1)
     return fail(KDECAY_ELAYOUT, "channel (d) stride must be 1");

@@ -30,8 +30,23 @@ _DTYPE_CODE = {
     torch.float16: _lib.KDECAY_F16,
 }
 
-# Head dims of the chunked (vector) kernels; others use the sequential kernel.
-VECTOR_HEAD_DIMS = (16, 32, 64, 128, 256)
+
+def chunked_head_dim(D: int, dtype: torch.dtype) -> bool:
+    """Head dims the chunked kernels take as they are: 16, 32, or a multiple of
+    one 128-byte channel group (64 bf16/fp16 or 32 fp32 channels).  Other head
+    dims are zero-padded to the next such size on the way in (channels are
+    independent, so the padding changes no value) and sliced on the way out."""
+    full = 128 // torch.empty((), dtype=dtype).element_size()
+    return D in (16, 32) or (D > 0 and D % full == 0)
+
+
+def _padded_head_dim(D: int, dtype: torch.dtype) -> int:
+    if D <= 16:
+        return 16
+    if D <= 32:
+        return 32
+    full = 128 // torch.empty((), dtype=dtype).element_size()
+    return -(-D // full) * full
 
 # One zero-initialised workspace per (device, stream); the kernels keep it
 # consistent from launch to launch, so it is never cleared again.
@@ -177,13 +192,16 @@ class _ScanFn(torch.autograd.Function):
     """The chunked scan with a backward (kdecay_scan_fwd_train / kdecay_scan_bwd).
 
     Inputs: lam (fp32 [H], differentiable), V, init (fp32 [B,H,D] or None),
-    t_offset, out dtype.  Outputs: (y, final state).  The reference's GPU path
-    has no backward; its CPU path is differentiated by torch autograd through
-    triton_ops.py:240-246, which this replaces on HIP tensors.
+    t_offset, out dtype, sequential.  Outputs: (y, final state).  The
+    reference's GPU path has no backward; its CPU path is differentiated by
+    torch autograd through triton_ops.py:240-246, which this replaces on HIP
+    tensors.  With sequential=True, y and the final state are then rewritten
+    by the sequential kernel (its bits), while the backward uses the states
+    the chunked training forward saved (equal to tolerance).
     """
 
     @staticmethod
-    def forward(ctx, lam32, V, init32, t_offset, out_dtype):
+    def forward(ctx, lam32, V, init32, t_offset, out_dtype, sequential=False):
         B, H, N, D = V.shape
         dev = V.device
         v_code = _DTYPE_CODE[V.dtype]
@@ -209,6 +227,15 @@ class _ScanFn(torch.autograd.Function):
                 ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, stream,
             )
         _lib.check(rc, "kdecay_scan_fwd_train")
+        if sequential:
+            with _on_device(dev):
+                rc = lib.kdecay_scan_fwd_sequential(
+                    Vk.data_ptr(), v_code, _lib.strides4(Vk.stride()),
+                    out.data_ptr(), o_code, _lib.strides4(out.stride()),
+                    lam32.data_ptr(), init32.data_ptr() if init32 is not None else None, final.data_ptr(),
+                    B, H, N, D, int(t_offset), _stream_ptr(dev),
+                )
+            _lib.check(rc, "kdecay_scan_fwd_sequential")
         ctx.t_offset = int(t_offset)
         ctx.has_init = init32 is not None
         ctx.save_for_backward(lam32, Vk, init32 if init32 is not None else final.new_empty(0), states)
@@ -247,7 +274,7 @@ class _ScanFn(torch.autograd.Function):
                 ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, stream,
             )
         _lib.check(rc, "kdecay_scan_bwd")
-        return dlam, dV, dinit, None, None
+        return dlam, dV, dinit, None, None, None
 
 
 def _needs_grad(*ts) -> bool:
@@ -273,10 +300,13 @@ def global_decay_scan(
     Returns y ([B,H,N,D], dtype out_dtype or V.dtype, laid out like V), and
     with return_final_state also s_{N-1} ([B,H,D] fp32).
     algorithm: "chunked" (default) or "sequential" (the cross-check kernel).
-    Gradients (when lam, V or initial_state requires grad) need the chunked
-    scan.  The backward kernel takes the upstream gradient in V's dtype: with
-    out_dtype=float32 for a bf16/fp16 V, that gradient is rounded to V's dtype
-    first.
+    Head dims the chunked kernels do not take (chunked_head_dim) are
+    zero-padded to the next one they do.  When lam, V or initial_state
+    requires grad, the result carries a backward for every head dim, layout,
+    algorithm and out= (the gradients always come from the chunked backward
+    kernel).  The backward kernel takes the upstream gradient in V's dtype:
+    with out_dtype=float32 for a bf16/fp16 V, that gradient is rounded to V's
+    dtype first.
     """
     _require_hip(V, "V")
     if V.dim() != 4:
@@ -309,44 +339,88 @@ def global_decay_scan(
     lib = _lib.load()
     with _on_device(dev):
         stream = _stream_ptr(dev)
-        init_p = init32.data_ptr() if init32 is not None else None
-        fin_p = final.data_ptr() if final is not None else None
-        if algorithm == "sequential" or D not in VECTOR_HEAD_DIMS:
+        if algorithm == "sequential":
             rc = lib.kdecay_scan_fwd_sequential(
                 V.data_ptr(), v_code, _lib.strides4(V.stride()),
                 out.data_ptr(), o_code, _lib.strides4(out.stride()),
-                lam32.data_ptr(), init_p, fin_p, B, H, N, D, int(t_offset), stream,
+                lam32.data_ptr(), init32.data_ptr() if init32 is not None else None,
+                final.data_ptr() if final is not None else None, B, H, N, D, int(t_offset), stream,
             )
             _lib.check(rc, "kdecay_scan_fwd_sequential")
-        else:
-            Vk = V if _vector_layout_ok(V) else V.contiguous()
-            outk = out if _vector_layout_ok(out) else torch.empty(V.shape, dtype=out.dtype, device=dev)
-            nbytes = _fwd_workspace_bytes(lib, B, H, N, D, v_code)
-            ws = _workspace(dev, stream, nbytes)
-            rc = lib.kdecay_scan_fwd(
-                Vk.data_ptr(), v_code, _lib.strides4(Vk.stride()),
-                outk.data_ptr(), o_code, _lib.strides4(outk.stride()),
-                lam32.data_ptr(), init_p, fin_p, B, H, N, D, int(t_offset),
-                ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
-                stream,
-            )
-            _lib.check(rc, "kdecay_scan_fwd")
-            if outk is not out:
-                out.copy_(outk)
+        elif chunked_head_dim(D, V.dtype):
+            _chunked(lib, V, v_code, out, o_code, lam32, init32, final, t_offset, stream, dev)
+        else:  # zero channels up to a head dim the chunked kernels take
+            Dp = _padded_head_dim(D, V.dtype)
+            Vp = V.new_zeros((B, H, N, Dp))
+            Vp[..., :D] = V
+            initp = None
+            if init32 is not None:
+                initp = init32.new_zeros((B, H, Dp))
+                initp[..., :D] = init32
+            outp = torch.empty((B, H, N, Dp), dtype=out.dtype, device=dev)
+            finp = torch.empty((B, H, Dp), dtype=torch.float32, device=dev) if final is not None else None
+            _chunked(lib, Vp, v_code, outp, o_code, lam32, initp, finp, t_offset, stream, dev)
+            out.copy_(outp[..., :D])
+            if final is not None:
+                final.copy_(finp[..., :D])
     if return_final_state:
         return out, final
     return out
 
 
+def _chunked(lib, V, v_code, out, o_code, lam32, init32, final, t_offset, stream, dev) -> None:
+    """kdecay_scan_fwd on V into out (through contiguous copies where the
+    layout is not one the vector kernel takes)."""
+    B, H, N, D = V.shape
+    Vk = V if _vector_layout_ok(V) else V.contiguous()
+    outk = out if _vector_layout_ok(out) else torch.empty(V.shape, dtype=out.dtype, device=dev)
+    nbytes = _fwd_workspace_bytes(lib, B, H, N, D, v_code)
+    ws = _workspace(dev, stream, nbytes)
+    rc = lib.kdecay_scan_fwd(
+        Vk.data_ptr(), v_code, _lib.strides4(Vk.stride()),
+        outk.data_ptr(), o_code, _lib.strides4(outk.stride()),
+        lam32.data_ptr(), init32.data_ptr() if init32 is not None else None,
+        final.data_ptr() if final is not None else None, B, H, N, D, int(t_offset),
+        ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
+        stream,
+    )
+    _lib.check(rc, "kdecay_scan_fwd")
+    if outk is not out:
+        out.copy_(outk)
+
+
 def _scan_with_grad(lam, V, initial_state, return_final_state, t_offset, out, out_dtype, algorithm):
-    """global_decay_scan when a gradient is required: the chunked scan under _ScanFn."""
+    """global_decay_scan when a gradient is required: the chunked training
+    forward and backward under _ScanFn, with differentiable zero-padding of
+    the channels for head dims the kernels do not take, and a differentiable
+    copy into `out` when one is given."""
     B, H, N, D = V.shape
     dev = V.device
-    if algorithm != "chunked" or D not in VECTOR_HEAD_DIMS or out is not None:
-        raise NotImplementedError(
-            "kilat_amd: gradients need the chunked scan (algorithm='chunked', D in "
-            f"{VECTOR_HEAD_DIMS}, no out=); got algorithm={algorithm!r}, D={D}, out given={out is not None}"
-        )
+    if algorithm not in ("chunked", "sequential"):
+        raise ValueError(f"kilat_amd: unknown algorithm {algorithm!r}")
+    if out is not None:
+        _require_hip(out, "out")
+        if out.shape != V.shape or out.device != dev:
+            raise ValueError("kilat_amd: out must have V's shape and device")
+        if out_dtype is not None and out_dtype != out.dtype:
+            raise TypeError("kilat_amd: out_dtype and out.dtype differ")
+        y, final = _scan_with_grad(lam, V, initial_state, True, t_offset, None, out.dtype, algorithm)
+        out.copy_(y)
+        return (out, final) if return_final_state else out
+    if not chunked_head_dim(D, V.dtype):
+        Dp = _padded_head_dim(D, V.dtype)
+        Vp = torch.nn.functional.pad(V, (0, Dp - D))
+        initp = None
+        if initial_state is not None:
+            _require_hip(initial_state, "initial_state")
+            if tuple(initial_state.shape) != (B, H, D):
+                raise ValueError(f"kilat_amd: initial_state must be [B,H,D]={B, H, D}")
+            initp = torch.nn.functional.pad(initial_state, (0, Dp - D))
+        yp, finp = _scan_with_grad(lam, Vp, initp, True, t_offset, None, out_dtype, algorithm)
+        y = torch.empty_like(V, dtype=yp.dtype)
+        y.copy_(yp[..., :D])  # laid out like V, as empty_like(V) is in the reference
+        final = finp[..., :D].contiguous()
+        return (y, final) if return_final_state else y
     _require_hip(lam, "lam_scores")
     if lam.numel() != H:
         raise ValueError(f"kilat_amd: lam_scores has {lam.numel()} elements, V has {H} heads")
@@ -360,7 +434,7 @@ def _scan_with_grad(lam, V, initial_state, return_final_state, t_offset, out, ou
     o_dtype = out_dtype or V.dtype
     if o_dtype not in (V.dtype, torch.float32):
         raise TypeError("kilat_amd: out dtype must be V's dtype or float32")
-    y, final = _ScanFn.apply(lam32, V, init32, int(t_offset), o_dtype)
+    y, final = _ScanFn.apply(lam32, V, init32, int(t_offset), o_dtype, algorithm == "sequential")
     if return_final_state:
         return y, final
     return y
@@ -444,4 +518,4 @@ def decay_step(
 
 
 __all__ = ["triton_global_decay", "decay_step", "global_decay_scan", "workspace_error", "reserve_workspace",
-           "VECTOR_HEAD_DIMS"]
+           "chunked_head_dim"]

@@ -213,3 +213,33 @@ def test_integration_doc_holds_the_tested_ctypes_stub():
     if not os.path.exists(doc):
         pytest.skip("INTEGRATION.md is not in this copy of the tree")
     assert STUB_SOURCE in open(doc).read()
+
+
+def test_chunked_head_dims_and_padding():
+    """The chunked kernels take D = 16, 32 or a multiple of one 128-byte channel
+    group; the shim pads any other D to the next such size."""
+    import torch
+
+    from kilat_amd.triton_ops import _padded_head_dim, chunked_head_dim
+
+    for dt, full in ((torch.bfloat16, 64), (torch.float16, 64), (torch.float32, 32)):
+        for D in (16, 32, full, 2 * full, 3 * full, 8 * full):
+            assert chunked_head_dim(D, dt), (dt, D)
+            assert _padded_head_dim(D, dt) == D
+        for D in (1, 8, 15, 17, 31, 33, full + 1, 3 * full - 1):
+            assert not chunked_head_dim(D, dt), (dt, D)
+            p = _padded_head_dim(D, dt)
+            assert p >= D and chunked_head_dim(p, dt) and p - D < full, (dt, D, p)
+
+
+def test_library_takes_the_same_head_dims(kdecay_lib):
+    """kdecay_scan_workspace_bytes is non-zero exactly for the head dims the
+    shim sends to the chunked kernels (several chunks per stream here)."""
+    import torch
+
+    from kilat_amd.triton_ops import chunked_head_dim
+
+    for dt, code in ((torch.bfloat16, _lib.KDECAY_BF16), (torch.float32, _lib.KDECAY_F32)):
+        for D in range(1, 400):
+            ok = kdecay_lib.kdecay_scan_workspace_bytes(2, 3, 100000, D, code) > 0
+            assert ok == chunked_head_dim(D, dt), (dt, D)

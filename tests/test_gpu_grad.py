@@ -304,3 +304,54 @@ def test_graph_capture_backward_replays(hip_device, kdecay_lib, N):
         assert torch.equal(dlam, ref[1]), r
     with torch.cuda.stream(stream):
         assert kilat_amd.workspace_error(V) == 0
+
+
+@pytest.mark.parametrize("dname,D", [("f32", 1), ("f32", 48), ("bf16", 8), ("bf16", 48), ("bf16", 96), ("f16", 100),
+                                     ("f32", 96), ("bf16", 384), ("f32", 288)])
+def test_backward_any_head_dim(hip_device, kdecay_lib, dname, D):
+    """Every head dim has a backward (the reference's CPU path is differentiable
+    for any D): dims the chunked kernels do not take are zero-padded in a
+    differentiable way; 384 (bf16) and 288 (fp32) exercise heads of several
+    128-byte channel groups beyond 256.  With a carried state, a final-state
+    gradient and an offset."""
+    dtype = DTYPES[dname]
+    g = torch.Generator().manual_seed(230 + D)
+    lam = lam_uniform(3, 0.5, 0.999, g)
+    for N in (5, 700):
+        V = torch.randn(2, 3, N, D, generator=g).to(dtype)
+        gy = torch.randn(2, 3, N, D, generator=g).to(dtype)
+        init = torch.randn(2, 3, D, generator=g)
+        gfin = torch.randn(2, 3, D, generator=g)
+        dv, dl, di = gpu_grads(lam, V, gy, hip_device, init=init, gfin=gfin, t_offset=9)
+        rdv, rdl, rdi = oracle_grads(lam, V, gy, init=init, gfin=gfin, t_offset=9)
+        assert dv.shape == V.shape and dv.dtype == dtype
+        check(dv, dl, di, rdv, rdl, rdi, dtype, f"D={D} N={N}")
+
+
+@pytest.mark.parametrize("D", [64, 40])
+def test_backward_sequential_and_out(hip_device, kdecay_lib, D):
+    """algorithm='sequential' and out= keep their forward results (the
+    sequential kernel's bits; the given tensor filled) and still carry the
+    backward, against fp64 autograd through the oracle."""
+    g = torch.Generator().manual_seed(240 + D)
+    lam = lam_uniform(4, 0.5, 0.999, g)
+    V = torch.randn(2, 4, 900, D, generator=g)
+    gy = torch.randn(2, 4, 900, D, generator=g)
+    rdv, rdl, _ = oracle_grads(lam, V, gy)
+    y_seq_nograd = kilat_amd.global_decay_scan(lam.to(hip_device), V.to(hip_device), algorithm="sequential")
+    for kw in ({"algorithm": "sequential"}, {"out": "given"}):
+        lam_d = lam.to(hip_device).requires_grad_(True)
+        V_d = V.to(hip_device).requires_grad_(True)
+        out = None
+        if kw.get("out") == "given":
+            out = torch.empty(V.shape, device=hip_device)
+            kw = {"out": out}
+        print(f"  grad D={D} {list(kw)}", flush=True)
+        y = kilat_amd.global_decay_scan(lam_d, V_d, **kw)
+        if out is not None:
+            assert y is out
+        else:
+            assert torch.equal(y.detach(), y_seq_nograd)
+        (y * gy.to(hip_device)).sum().backward()
+        torch.cuda.synchronize()
+        check(V_d.grad.cpu(), lam_d.grad.cpu(), None, rdv, rdl, None, torch.float32, f"D={D} {list(kw)}")

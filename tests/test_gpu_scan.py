@@ -481,3 +481,30 @@ def test_native_c_abi_caller(hip_device, kdecay_lib):
     print(r.stdout.strip(), flush=True)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "c_abi_check OK" in r.stdout
+
+
+@pytest.mark.parametrize("dname,D", [("bf16", 384), ("f32", 96), ("f32", 288), ("bf16", 48), ("f16", 8),
+                                     ("f32", 1), ("bf16", 100)])
+def test_scan_wide_and_padded_head_dims(hip_device, kdecay_lib, dname, D):
+    """Head dims of several 128-byte channel groups (bf16 384, fp32 96 and 288)
+    run on the chunked kernels as they are; others (48, 8, 1, 100) are
+    zero-padded by the shim to the next head dim the kernels take.  Against
+    the oracle, with a carried state and an offset, on contiguous V and on the
+    projection's (B,N,H*D) view."""
+    dtype = DTYPES[dname]
+    g = torch.Generator().manual_seed(260 + D)
+    lam = lam_uniform(3, 0.5, 0.9999, g)
+    assert kilat_amd.chunked_head_dim(D, dtype) == (D in (384, 96, 288))
+    for N in (3, 1300):
+        for fused in (False, True):
+            if fused:
+                V = torch.randn(2, N, 3, D, generator=g).to(dtype).transpose(1, 2)
+            else:
+                V = torch.randn(2, 3, N, D, generator=g).to(dtype)
+            init = torch.randn(2, 3, D, generator=g)
+            y, fin = gpu_scan(lam, V, hip_device, return_final_state=True, initial_state=init.to(hip_device),
+                              t_offset=5)
+            ref, sref = O.scan(lam, V, init, 5)
+            assert y.shape == V.shape and y.dtype == dtype and y.stride() == V.stride()
+            assert_parity(y, ref, dtype, f"D={D} N={N} fused={fused}")
+            assert rel_err(fin, sref) <= 1e-5
