@@ -453,7 +453,7 @@ __device__ __forceinline__ int rotated_stream(int j, int rot, int nstream) {
 // Items are numbered chunk-major (item = chunk * nstream + j, j rotated to
 // the stream by the chunk index; see rotated_stream), so the chunk an item
 // waits on always has a smaller item number.
-template <typename TI, typename TO, int LPR, int R, int NW, int W>
+template <typename TI, typename TO, int LPR, int R, int NW, int W, bool FZ>
 struct ChunkScan {
   static constexpr int VW = 16 / (int)sizeof(TI);  // channels per lane
   static constexpr int DG = LPR * VW;  // channels of one stream
@@ -463,6 +463,7 @@ struct ChunkScan {
   static constexpr int NT = NW * 64;
   static constexpr int DQ = (DG + 63) / 64;
   static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "LPR must divide 64");
+  static_assert(DG <= 64, "wavefront 0 holds one channel of the stream per lane");
   static_assert(G + 1 <= NT, "power table is filled one entry per thread");
 
   struct Smem {
@@ -481,12 +482,25 @@ struct ChunkScan {
   // Returns the item's decay factor, loaded first: memory operations retire
   // in issue order, so its first use then waits for it alone, not for the
   // rows, and the per-head tables are computed while the rows are in flight.
-  __device__ static float load(const ScanArgs& a, int item, uint4 (&raw)[R]) {
+  // `init` receives the carry-in state of channel `lane` of the stream (the
+  // caller's initial state on chunk 0, else 0).  It is loaded here, ahead of
+  // the rows and unconditionally (a.lam stands in when there is nothing to
+  // load): loaded later, under a condition, it left the compiler unsure at the
+  // look-back's join whether the load was still pending, and it waited there
+  // for every memory operation, the chunk's own look-back publishes included
+  // (a device-scope store round trip on every chunk's critical path).
+  __device__ static float load(const ScanArgs& a, int item, uint4 (&raw)[R], float& init) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int chunk = item / a.nstream, stream = rotated_stream(item % a.nstream, chunk % a.nstream, a.nstream);
     const int64_t bh = stream / a.ng, grp = stream % a.ng;
     const int64_t b = bh / a.H, h = bh % a.H;
     const float lam = a.lam[h];
+    {
+      const bool has = chunk == 0 && a.init != nullptr;
+      const float* ip = has ? a.init + bh * a.D + grp * DG + (lane < DG ? lane : DG - 1) : a.lam;
+      const float v = *ip;
+      init = has ? v : 0.0f;
+    }
     const int ds = lane % LPR, gw = lane / LPR;
     const int64_t rbase = (int64_t)chunk * L + (int64_t)(wave * GW + gw) * R;
     const TI* vp = static_cast<const TI*>(a.V) + b * a.vb + h * a.vh + grp * DG + (int64_t)ds * VW;
@@ -502,8 +516,8 @@ struct ChunkScan {
   // launch generation every workgroup read before publishing anything.
   // Tables, chunk reduction and look-back: st = the state before this lane's
   // first row.
-  __device__ static void scan_chunk(const ScanArgs& a, int item, uint4 (&raw)[R], float lam, unsigned epoch,
-                                    Smem& sm, float (&st)[VW]) {
+  __device__ static void scan_chunk(const ScanArgs& a, int item, uint4 (&raw)[R], float lam, float init,
+                                    unsigned epoch, Smem& sm, float (&st)[VW]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const bool multi = a.nchunk > 1;
     const int chunk = item / a.nstream, stream = rotated_stream(item % a.nstream, chunk % a.nstream, a.nstream);
@@ -519,7 +533,7 @@ struct ChunkScan {
     __syncthreads();
     if (tid <= G) sm.pw[tid] = pow_like_torch(lam, (int64_t)tid * R);
     for (int r = tid; r < L; r += NT) {
-      if (row0 + r < a.N) sm.rz[r] = 1.0f / z_of(lam, a.t_offset + row0 + r);
+      if (row0 + r < a.N) sm.rz[r] = 1.0f / (FZ ? z_of_fast(lam, a.t_offset + row0 + r) : z_of(lam, a.t_offset + row0 + r));
     }
 
     // Sequential pass over the lane's rows (zero carry in).
@@ -564,7 +578,7 @@ struct ChunkScan {
         if (d < DG) {
 #pragma unroll
           for (int w = 0; w < NW; ++w) agg[q] = __builtin_fmaf(mW, agg[q], sm.wt[w][d]);
-          if (chunk == 0 && a.init) carry[q] = a.init[c0 + d];
+          if (q == 0) carry[q] = init;  // DG <= 64: one channel per lane
           if (chunk > 0 && !last) publish(base + (int64_t)chunk * DG + d, tag_agg, agg[q]);
         }
       }
@@ -653,10 +667,10 @@ struct ChunkScan {
     }
   }
 
-  __device__ static void process(const ScanArgs& a, int item, uint4 (&raw)[R], float lam, unsigned epoch,
-                                 Smem& sm) {
+  __device__ static void process(const ScanArgs& a, int item, uint4 (&raw)[R], float lam, float init,
+                                 unsigned epoch, Smem& sm) {
     float st[VW];
-    scan_chunk(a, item, raw, lam, epoch, sm, st);
+    scan_chunk(a, item, raw, lam, init, epoch, sm, st);
     store_chunk(a, item, raw, lam, st, sm);
   }
 };
@@ -672,15 +686,16 @@ __device__ __forceinline__ unsigned read_epoch(const ScanArgs& a) {
 // items with smaller indices, which are dispatched first (workgroups are
 // dispatched in index order on each XCD), so the smallest unfinished item
 // can always run: no co-residency requirement and no ticket counter.
-template <typename TI, typename TO, int LPR, int R, int NW, int W, int WPE>
+template <typename TI, typename TO, int LPR, int R, int NW, int W, int WPE, bool FZ>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, 8)))
 void scan_chunked(ScanArgs a) {
-  using CS = ChunkScan<TI, TO, LPR, R, NW, W>;
+  using CS = ChunkScan<TI, TO, LPR, R, NW, W, FZ>;
   __shared__ typename CS::Smem sm;
   const unsigned epoch = read_epoch(a);
   uint4 raw[R];
-  const float lam = CS::load(a, blockIdx.x, raw);
-  CS::process(a, blockIdx.x, raw, lam, epoch, sm);
+  float init;
+  const float lam = CS::load(a, blockIdx.x, raw, init);
+  CS::process(a, blockIdx.x, raw, lam, init, epoch, sm);
 }
 
 // --------------------------------------------------------------------------
@@ -1269,7 +1284,7 @@ bool dtype_ok(int dt) { return dt == KDECAY_F32 || dt == KDECAY_BF16 || dt == KD
 
 // Launch shape of the chunked scan: a chunk holds NW * 64 lanes x R rows x
 // 16 bytes = 64 KiB of input whatever the dtype and D, in 64 VGPRs per lane
-// (half that for small grids; see rows_per_lane).  Measured on MI355X at B=8
+// (half that for small grids; see chunk_shape).  Measured on MI355X at B=8
 // N=4096 H=12 D=64 and B=1 N=65536 H=16 D=128 bf16 against R in {2..32}, NW
 // in {2,4,8}: this is the fastest.
 constexpr int kR = 16;
@@ -1322,24 +1337,32 @@ int64_t group_width(int v_dtype, int64_t D) {
   return D < full ? D : full;
 }
 
-int64_t chunk_rows(int v_dtype, int64_t D, int R) {
+// Chunk shape: R rows per lane, NW wavefronts per workgroup.
+struct ChunkShape {
+  int R, NW;
+};
+
+int64_t chunk_rows(int v_dtype, int64_t D, ChunkShape c) {
   const int64_t vw = 16 / elem_size(v_dtype);
   const int64_t lpr = group_width(v_dtype, D) / vw;
-  return kNW * (64 / lpr) * R;
+  return c.NW * (64 / lpr) * c.R;
 }
 
-// Rows per lane for a problem: kR, or kRSmall when a kR-row grid would have
-// at most kSmallGrid chunks and leave most of the device idle.  Measured on
-// MI355X (bf16, D=64/128): 8 rows per lane were 10-18% faster for grids of
-// 96-384 chunks at 16 rows, and 6-7% slower for grids of 768-1024.  The rule
-// uses the shape only, so kdecay_scan_workspace_bytes can apply it too.
+// Chunk shape of a problem: (kR, kNW), or (kRSmall, kNWSmall) when a
+// (kR, kNW) grid would have at most kSmallGrid chunks and leave most of the
+// device idle.  Measured on MI355X (bf16, D=64/128): 8 rows per lane were
+// 10-18% faster for grids of 96-384 chunks at 16 rows, and 6-7% slower for
+// grids of 768-1024.  The rule uses the shape only, so
+// kdecay_scan_workspace_bytes can apply it too.
 constexpr int kRSmall = 8;
+constexpr int kNWSmall = 4;
 constexpr int64_t kSmallGrid = 512;
 
-int rows_per_lane(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
-  const int64_t L = chunk_rows(v_dtype, D, kR);
+ChunkShape chunk_shape(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
+  const int64_t L = chunk_rows(v_dtype, D, ChunkShape{kR, kNW});
   const int64_t nstream = B * H * (D / group_width(v_dtype, D));
-  return (N + L - 1) / L * nstream <= kSmallGrid ? kRSmall : kR;
+  if ((N + L - 1) / L * nstream <= kSmallGrid) return ChunkShape{kRSmall, kNWSmall};
+  return ChunkShape{kR, kNW};
 }
 
 // Head dims of the chunked kernels: 16, 32, or any multiple of a full
@@ -1355,33 +1378,54 @@ template <typename TI, typename TO, int DG, int R = kR, int NW = kNW, int WPE = 
 int launch_chunked(const ScanArgs& a, int64_t grid, hipStream_t s) {
   constexpr int VW = 16 / (int)sizeof(TI);
   constexpr int LPR = DG / VW;
-  auto* const one_round = scan_chunked<TI, TO, LPR, R, NW, kW, WPE>;
-  auto* const rounds = scan_chunked<TI, TO, LPR, R, NW, kWRounds, WPE>;
-  static const int per_cu = workgroups_per_cu(reinterpret_cast<const void*>(one_round), NW * 64);
-  const int64_t resident = (int64_t)per_cu * cu_count();
-  if (resident > 0 && grid > resident)
-    hipLaunchKernelGGL(rounds, dim3((unsigned)grid), dim3(NW * 64), 0, s, a);
-  else
-    hipLaunchKernelGGL(one_round, dim3((unsigned)grid), dim3(NW * 64), 0, s, a);
+  // Small grids are latency-bound: there the per-row normaliser table uses
+  // the unrolled, branch-free power (B=8 N=1024 H=6 D=64 bf16: 7.07 -> 6.85
+  // us); for large grids the loop form is cheaper (B=8 N=4096 H=12 D=64:
+  // 18.36 vs 18.74 us with the unrolled one).  Same values either way.
+  constexpr bool FZ = R == kRSmall && NW == kNWSmall;
+  if constexpr (FZ) {
+    // Small grids run in one round.  Long chains of few streams want a wide
+    // window: a chunk then folds the aggregates of its predecessors, each
+    // published as soon as that chunk is scanned, instead of waiting for their
+    // inclusive prefixes hop by hop.  Measured (bf16 D=64, same-box A/B,
+    // window 4 / 8 / 16): B=1 N=32768 H=6 (128 chunks per stream) 27.97 /
+    // 19.44 / 15.75 us; B=1 N=16384 H=12 (64) 17.45 / 13.81 / 12.49 us; B=1
+    // N=8192 H=6 (32) 11.33 / 9.40 / 8.65 us; B=2 N=4096 H=12 (16) 8.99 /
+    // 8.23 / -; B=8 N=1024 H=6 (4 chunks per stream) 7.00 / 6.89 / -.
+    auto* const k = a.nchunk > 16 ? scan_chunked<TI, TO, LPR, R, NW, 16, WPE, FZ>
+                  : a.nchunk > 4 ? scan_chunked<TI, TO, LPR, R, NW, 8, WPE, FZ>
+                                 : scan_chunked<TI, TO, LPR, R, NW, kW, WPE, FZ>;
+    hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(NW * 64), 0, s, a);
+  } else {
+    auto* const one_round = scan_chunked<TI, TO, LPR, R, NW, kW, WPE, FZ>;
+    auto* const rounds = scan_chunked<TI, TO, LPR, R, NW, kWRounds, WPE, FZ>;
+    static const int per_cu = workgroups_per_cu(reinterpret_cast<const void*>(one_round), NW * 64);
+    const int64_t resident = (int64_t)per_cu * cu_count();
+    if (resident > 0 && grid > resident)
+      hipLaunchKernelGGL(rounds, dim3((unsigned)grid), dim3(NW * 64), 0, s, a);
+    else
+      hipLaunchKernelGGL(one_round, dim3((unsigned)grid), dim3(NW * 64), 0, s, a);
+  }
   return hip_check("scan_chunked launch");
 }
 
-// DG: channels per stream (group_width); R: rows per lane (rows_per_lane).
-template <typename TI, typename TO, int R>
+// DG: channels per stream (group_width); R, NW: the chunk shape (chunk_shape).
+template <typename TI, typename TO, int R, int NW>
 int dispatch_dg_r(const ScanArgs& a, int64_t DG, int64_t grid, hipStream_t s) {
   switch (DG) {
-    case 16: return launch_chunked<TI, TO, 16, R>(a, grid, s);
-    case 32: return launch_chunked<TI, TO, 32, R>(a, grid, s);
+    case 16: return launch_chunked<TI, TO, 16, R, NW>(a, grid, s);
+    case 32: return launch_chunked<TI, TO, 32, R, NW>(a, grid, s);
     case 64:
-      if constexpr (sizeof(TI) == 2) return launch_chunked<TI, TO, 64, R>(a, grid, s);
+      if constexpr (sizeof(TI) == 2) return launch_chunked<TI, TO, 64, R, NW>(a, grid, s);
       break;
   }
   return fail(KDECAY_ESHAPE, "unsupported channel group %lld", (long long)DG);
 }
 
 template <typename TI, typename TO>
-int dispatch_dg(const ScanArgs& a, int64_t DG, int64_t grid, hipStream_t s, int R) {
-  return R == kRSmall ? dispatch_dg_r<TI, TO, kRSmall>(a, DG, grid, s) : dispatch_dg_r<TI, TO, kR>(a, DG, grid, s);
+int dispatch_dg(const ScanArgs& a, int64_t DG, int64_t grid, hipStream_t s, ChunkShape c) {
+  if (c.R == kRSmall && c.NW == kNWSmall) return dispatch_dg_r<TI, TO, kRSmall, kNWSmall>(a, DG, grid, s);
+  return dispatch_dg_r<TI, TO, kR, kNW>(a, DG, grid, s);
 }
 
 // Launch shape of the backward scan: 4 rows per lane (it holds V, gy and g
@@ -1521,7 +1565,7 @@ int kdecay_debug_set_spin_limit(int polls) {
 
 size_t kdecay_scan_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   if (B <= 0 || H <= 0 || N <= 0 || !dtype_ok(v_dtype) || !head_dim_ok(v_dtype, D)) return 0;
-  const int64_t L = chunk_rows(v_dtype, D, rows_per_lane(B, H, N, D, v_dtype));
+  const int64_t L = chunk_rows(v_dtype, D, chunk_shape(B, H, N, D, v_dtype));
   const int64_t nchunk = (N + L - 1) / L;
   if (nchunk <= 1) return 0;
   return kHeaderBytes + (size_t)(B * H * nchunk * D) * sizeof(u64);
@@ -1550,8 +1594,8 @@ static int scan_fwd_impl(const void* V, int v_dtype, const int64_t* v_strides, v
       return fail(KDECAY_ELAYOUT, "stride %d is not a multiple of 16 bytes", k);
   }
 
-  const int R = rows_per_lane(B, H, N, D, v_dtype);
-  const int64_t L = chunk_rows(v_dtype, D, R);
+  const ChunkShape shape = chunk_shape(B, H, N, D, v_dtype);
+  const int64_t L = chunk_rows(v_dtype, D, shape);
   const int64_t nchunk = (N + L - 1) / L;
   const int64_t DG = group_width(v_dtype, D);
   const int64_t nstream = B * H * (D / DG);
@@ -1589,13 +1633,13 @@ static int scan_fwd_impl(const void* V, int v_dtype, const int64_t* v_strides, v
   a.nsaved = (N + a.state_rows - 1) / a.state_rows;
   a.states = a.nsaved > 1 ? states : nullptr;
 
-  if (v_dtype == KDECAY_F32) return dispatch_dg<float, float>(a, DG, grid, s, R);
+  if (v_dtype == KDECAY_F32) return dispatch_dg<float, float>(a, DG, grid, s, shape);
   if (v_dtype == KDECAY_BF16) {
-    if (out_dtype == KDECAY_BF16) return dispatch_dg<__bf16, __bf16>(a, DG, grid, s, R);
-    return dispatch_dg<__bf16, float>(a, DG, grid, s, R);
+    if (out_dtype == KDECAY_BF16) return dispatch_dg<__bf16, __bf16>(a, DG, grid, s, shape);
+    return dispatch_dg<__bf16, float>(a, DG, grid, s, shape);
   }
-  if (out_dtype == KDECAY_F16) return dispatch_dg<_Float16, _Float16>(a, DG, grid, s, R);
-  return dispatch_dg<_Float16, float>(a, DG, grid, s, R);
+  if (out_dtype == KDECAY_F16) return dispatch_dg<_Float16, _Float16>(a, DG, grid, s, shape);
+  return dispatch_dg<_Float16, float>(a, DG, grid, s, shape);
 }
 
 int kdecay_scan_fwd(const void* V, int v_dtype, const int64_t* v_strides, void* out, int out_dtype,

@@ -31,13 +31,16 @@ _DTYPE_CODE = {
 }
 
 
+# Channels of one full 128-byte channel group, per element type.
+_GROUP = {torch.float32: 32, torch.bfloat16: 64, torch.float16: 64}
+
+
 def chunked_head_dim(D: int, dtype: torch.dtype) -> bool:
     """Head dims the chunked kernels take as they are: 16, 32, or a multiple of
     one 128-byte channel group (64 bf16/fp16 or 32 fp32 channels).  Other head
     dims are zero-padded to the next such size on the way in (channels are
     independent, so the padding changes no value) and sliced on the way out."""
-    full = 128 // torch.empty((), dtype=dtype).element_size()
-    return D in (16, 32) or (D > 0 and D % full == 0)
+    return D == 16 or D == 32 or (D > 0 and D % _GROUP[dtype] == 0)
 
 
 def _padded_head_dim(D: int, dtype: torch.dtype) -> int:
@@ -45,7 +48,7 @@ def _padded_head_dim(D: int, dtype: torch.dtype) -> int:
         return 16
     if D <= 32:
         return 32
-    full = 128 // torch.empty((), dtype=dtype).element_size()
+    full = _GROUP[dtype]
     return -(-D // full) * full
 
 # One zero-initialised workspace per (device, stream); the kernels keep it
@@ -75,15 +78,16 @@ def _dtype_code(t: torch.Tensor, name: str) -> int:
 
 
 def _vector_layout_ok(t: torch.Tensor) -> bool:
-    """The chunked kernel's layout rule: d-stride 1, 16-byte rows and base."""
+    """The chunked kernel's layout rule: d-stride 1, 16-byte base, and every
+    other stride a multiple of 16 bytes (size-1 dims excepted).  Called only
+    for head dims the chunked kernels take, whose rows are whole 16-byte
+    vectors."""
+    if t.data_ptr() & 15:
+        return False
     vw = 16 // t.element_size()
-    if t.data_ptr() % 16:
-        return False
-    if t.is_contiguous():  # every stride is a multiple of D
-        return t.size(3) % vw == 0 or t.size(0) * t.size(1) * t.size(2) <= 1
-    if t.size(3) > 1 and t.stride(3) != 1:
-        return False
-    return all(t.size(k) == 1 or t.stride(k) % vw == 0 for k in range(3))
+    sz, st = t.shape, t.stride()
+    return ((st[3] == 1 or sz[3] == 1) and (st[2] % vw == 0 or sz[2] == 1) and (st[1] % vw == 0 or sz[1] == 1)
+            and (st[0] % vw == 0 or sz[0] == 1))
 
 
 if hasattr(torch._C, "_cuda_getCurrentRawStream"):

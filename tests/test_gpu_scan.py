@@ -508,3 +508,23 @@ def test_scan_wide_and_padded_head_dims(hip_device, kdecay_lib, dname, D):
             assert y.shape == V.shape and y.dtype == dtype and y.stride() == V.stride()
             assert_parity(y, ref, dtype, f"D={D} N={N} fused={fused}")
             assert rel_err(fin, sref) <= 1e-5
+
+
+@pytest.mark.parametrize("dname,H,N", [("bf16", 3, 2000), ("bf16", 2, 5000), ("bf16", 1, 40000), ("f32", 2, 9000),
+                                       ("f16", 1, 70000)])
+def test_small_grid_windows(hip_device, kdecay_lib, dname, H, N):
+    """Small grids (at most 512 chunks of 512 rows) of few streams with long
+    chains: the one-round launch takes a look-back window of 4, 8 or 16 by
+    chunks per stream (8 rows per lane: 256-row chunks for 128-byte groups).
+    Against the C restatement at full length, with a carried state and an
+    offset; the final state too."""
+    dtype = DTYPES[dname]
+    g = torch.Generator().manual_seed(280 + N)
+    lam = lam_uniform(H, 0.9, 0.99999, g)
+    V = torch.randn(1, H, N, 64, generator=g).to(dtype)
+    init = torch.randn(1, H, 64, generator=g)
+    y, fin = gpu_scan(lam, V, hip_device, return_final_state=True, initial_state=init.to(hip_device), t_offset=11)
+    ref, sref = C.scan_f32(lam.numpy(), V.float().numpy(), init.numpy(), 11)
+    assert_parity(y.cpu(), torch.from_numpy(ref).to(dtype), dtype, f"{dname} H={H} N={N}")
+    assert rel_err(fin.cpu(), torch.from_numpy(sref)) <= 1e-5
+    assert kilat_amd.workspace_error(V.to(hip_device)) == 0
