@@ -326,47 +326,101 @@ def bench_backward(torch, dev, steps=100):
 
 def bench_e2e(torch, dev, iters=5):
     """C5: KilatTransformer forward (768 wide, 12 layers, 6 decay + 6 MLA heads, MoE 8 x top-2,
-    vocab 50000), random init, bf16 autocast, B=8 N=1024, decay path on the HIP kernel.
-    Timed with the reference's glue (two .contiguous() copies around the op) and with
-    layout-fused I/O; the decay op's own share is timed with events around its calls."""
+    vocab 50000), random init, bf16 autocast, B=8 N=1024, decay path on the HIP kernel, with
+    the reference's glue (two .contiguous() copies around the op) and with layout-fused I/O.
+
+    The model is host-bound (its MoE expert loop synchronises with the host), so its
+    forward time hides the decay path; the path itself is timed apart, GPU-bound, by
+    decay_path_per_layer()."""
     import kilat_amd
     from tests.e2e_model import E2EConfig, KilatE2E
 
     torch.manual_seed(4)
     cfg = E2EConfig()
     B, N = 8, 1024
-    spans = []
-
-    def timed_decay(lam, V):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        y = kilat_amd.triton_global_decay(lam, V)
-        b.record()
-        spans.append((a, b))
-        return y
-
-    model = KilatE2E(cfg, timed_decay).to(dev).eval()
+    model = KilatE2E(cfg, kilat_amd.triton_global_decay).to(dev).eval()
     ids = torch.randint(0, cfg.vocab_size, (B, N), device=dev)
     out = {"config": "C5: n_embd=768 n_layer=12 n_head=12 recall_ratio=0.5 MoE 8 x top-2 (+2 shared) "
                      "vocab=50000, bf16 autocast, B=8 N=1024, random init"}
     for fused in (False, True):
-        model.set_decay(timed_decay, fused_layout=fused)
+        model.set_decay(kilat_amd.triton_global_decay, fused_layout=fused)
         with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
             for _ in range(2):
                 model(ids)
             torch.cuda.synchronize()
-            spans.clear()
             t = time.perf_counter()
             for _ in range(iters):
                 model(ids)
             torch.cuda.synchronize()
             sec = (time.perf_counter() - t) / iters
-        decay_ms = sum(a.elapsed_time(b) for a, b in spans) / iters
         key = "fused_layout" if fused else "reference_glue"
-        out[key] = {"ms_per_forward": round(sec * 1e3, 3), "tokens_per_s": round(B * N / sec, 1),
-                    "decay_ms_per_forward": round(decay_ms, 4),
-                    "decay_share_pct": round(100 * decay_ms / (sec * 1e3), 3)}
+        out[key] = {"ms_per_forward": round(sec * 1e3, 3), "tokens_per_s": round(B * N / sec, 1)}
+    out["decay_path_per_layer"] = decay_path_per_layer(torch, dev)
     return out
+
+
+def decay_path_per_layer(torch, dev, reps=200):
+    """One layer's decay path at the C5 shape, GPU-bound (many layers' worth of launches
+    back to back, 16 rotated projection buffers): from the v_proj_global output (B,N,H*D)
+    to the (B,N,H*D) input of the concatenation.  'reference_glue' is attention.py:368-374
+    (.view/.transpose/.contiguous(), the op, .transpose/.reshape: two copies and the scan),
+    'fused_layout' hands the op the strided view and takes its output back as a view (the
+    scan alone).  Also the scan alone on contiguous V, through the C ABI."""
+    import kilat_amd
+    from kilat_amd import _lib
+
+    B, N, H, D = 8, 1024, 6, 64
+    lam = c2_lam(H, torch).to(dev)
+    flats = [torch.randn(B, N, H * D, device=dev).to(torch.bfloat16) for _ in range(16)]
+
+    def glue(k):
+        V = flats[k % 16].view(B, N, H, D).transpose(1, 2).contiguous()
+        return kilat_amd.triton_global_decay(lam, V).transpose(1, 2).reshape(B, N, H * D)
+
+    def fused(k):
+        V = flats[k % 16].view(B, N, H, D).transpose(1, 2)
+        return kilat_amd.triton_global_decay(lam, V).transpose(1, 2).reshape(B, N, H * D)
+
+    lib = _lib.load()
+    conts = [f.view(B, N, H, D).transpose(1, 2).contiguous() for f in flats]
+    ys = [torch.empty_like(c) for c in conts]
+    from kilat_amd.triton_ops import _stream_ptr, _workspace
+
+    stream = _stream_ptr(dev)
+    ws = _workspace(dev, stream, lib.kdecay_scan_workspace_bytes(B, H, N, D, _lib.KDECAY_BF16))
+    args = [(c.data_ptr(), _lib.KDECAY_BF16, _lib.strides4(c.stride()), y.data_ptr(), _lib.KDECAY_BF16,
+             _lib.strides4(y.stride()), lam.data_ptr(), None, None, B, H, N, D, 0, ws.data_ptr(), ws.numel(), stream)
+            for c, y in zip(conts, ys)]
+
+    def scan_only(k):
+        lib.kdecay_scan_fwd(*args[k % 16])
+
+    res = {"config": "one layer at C5: B=8 N=1024 H=6 D=64 bf16, GPU-bound back-to-back, 16 rotated buffers"}
+    for name, fn in (("reference_glue", glue), ("fused_layout", fused), ("scan_only_c_abi", scan_only)):
+        # the graph keeps the host out of the measurement: reps layers captured once
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for k in range(4):
+                fn(k)  # eager warm-up on the capture stream (sizes its workspace)
+            if name == "scan_only_c_abi":  # its launches go to the capture stream from here on
+                args[:] = [a[:-1] + (side.cuda_stream,) for a in args]
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                for k in range(reps):
+                    fn(k)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(3):
+            g.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        res[name + "_us"] = round(t0.elapsed_time(t1) * 1e3 / (3 * reps), 3)
+        del g
+    return res
 
 
 def cpu_baseline(torch, B, H, N, D):
