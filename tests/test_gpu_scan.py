@@ -40,12 +40,19 @@ def gpu_scan(lam, V, dev, **kw):
 
 
 def assert_parity(y, ref, dtype, what=""):
+    """fp32: rel_err <= 1e-5.  bf16/fp16: max-abs <= 2e-2 (the target's bound),
+    and per (b,h) stream max|y-ref| / max|ref| <= 2e-2 as well, a few ulps of
+    the stream's own scale, so that a stream of small values (a head with lam
+    near 1 late in the sequence) cannot hide a dropped or wrong carry under
+    the absolute bound."""
     if dtype == torch.float32:
         e = rel_err(y, ref)
         assert e <= 1e-5, f"{what}: rel_err {e:.3e} > 1e-5"
     else:
         e = max_abs(y, ref)
         assert e <= 2e-2, f"{what}: max_abs {e:.3e} > 2e-2"
+        r = rel_err(y, ref)
+        assert r <= 2e-2, f"{what}: per-stream relative error {r:.3e} > 2e-2"
 
 
 @pytest.mark.parametrize("dname", ["f32", "bf16", "f16"])
@@ -202,6 +209,19 @@ def test_c2_bf16_full(hip_device, kdecay_lib):
     assert_parity(y, ref, torch.bfloat16, "C2")
     assert rel_err(fin, sref) <= 1e-5
     assert kilat_amd.workspace_error(V.to(hip_device)) == 0
+
+
+def test_c4_fp32_output_long_context(hip_device, kdecay_lib):
+    """C4 (D=128: two channel groups per head; 4096 chunks, several rounds)
+    with an fp32 output, against the oracle's fp32 output at the fp32
+    tolerance: late rows of the lam ~ 0.99999 heads are small, and only a
+    tight relative check sees their carries."""
+    lam, V = c4_inputs()
+    y, fin = gpu_scan(lam, V, hip_device, return_final_state=True, out_dtype=torch.float32)
+    ref, sref = O.scan(lam, V, out_dtype=torch.float32)
+    assert y.dtype == torch.float32
+    assert_parity(y, ref, torch.float32, "C4 fp32 out")
+    assert rel_err(fin, sref) <= 1e-5
 
 
 def test_c4_bf16_long_context(hip_device, kdecay_lib):
