@@ -420,10 +420,46 @@ __device__ __forceinline__ uint4 load16_stream(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Buffer resource over `rows` rows of a stream of DG channels, `stride`
+// elements apart (stride >= DG), starting at p: the range ends with the last
+// row's channels, so a buffer load of any later row returns zeros without
+// touching memory.  Offsets are 32-bit: the host keeps a chunk's rows within
+// 2^31 bytes.
+template <int DG, typename T>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_buffer(const T* p, int64_t rows, int64_t stride) {
+  const int64_t bytes = rows > 0 ? ((rows - 1) * stride + DG) * (int64_t)sizeof(T) : 0;
+  const int n = bytes > 0x7fffffffLL ? 0x7fffffff : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(p), (short)0, n, 0x00020000);
+}
+
+// 16-byte non-temporal buffer load at byte offset `off`.
+__device__ __forceinline__ uint4 load16_buffer(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// The launch epoch from the workspace header, kept in a vector register:
+// read through a uniform address, the value was moved to a scalar register
+// at once, which waited for the load (and every load issued before it).
+__device__ __forceinline__ unsigned read_epoch_v(const unsigned* hdr) {
+  unsigned zero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+  return __hip_atomic_load(const_cast<unsigned*>(hdr) + HDR_EPOCH + zero, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Keeps `x` opaque to the optimiser at this point, so values derived from it
 // are recomputed after the barrier rather than held in registers across it.
 __device__ __forceinline__ void opaque(uint4& x) {
   asm volatile("" : "+v"(x.x), "+v"(x.y), "+v"(x.z), "+v"(x.w));
+}
+
+// Pins the values of x at this point of the program: computations feeding
+// them are done before it and uses come after it (a row-by-row sweep then
+// stays row by row instead of running one chain ahead and holding its values).
+template <int N>
+__device__ __forceinline__ void pin(float (&x)[N]) {
+#pragma unroll
+  for (int j = 0; j < N; ++j) asm volatile("" : "+v"(x[j]));
 }
 
 // Stream of item j (0 <= j < nstream) of a chunk row rotated by `rot`.
@@ -706,12 +742,26 @@ void scan_chunked(ScanArgs a) {
 //   g_t  = u_t + lam * g_{t+1}           (reverse-time decay scan; g_N = 0)
 //   dV_t = g_t,  d(init) = lam * g_0
 //   dlam = sum_t g_t * s_{t-1} + sum_t gy_t * s_t * d(1/z_t)/dlam
-// One workgroup per chunk, chunks taken from the end of the sequence: the
-// reverse scan uses the forward scan's look-back with the chunk order
-// reversed.  s is recomputed inside each chunk from the state the forward
-// pass saved at the chunk's first row (ScanArgs::states), so no second
-// look-back is needed.  Each chunk writes its dlam partial; a second kernel
-// sums them per head in a fixed order (deterministic).
+// One workgroup per chunk, chunks taken from the end of the sequence: dV uses
+// the forward scan's look-back with the chunk order reversed.  s is
+// recomputed inside each chunk from the state the forward pass saved at the
+// chunk's first row (ScanArgs::states), so no second look-back is needed.
+//
+// dlam needs no row of V after the look-back.  For a lane's R rows t0 + i,
+// with sl / gl the lane-local scans started from zero (forward from the
+// lane's first row, reverse from its last), s_in = s_{t0-1} and
+// g_out = g_{t0+R}:
+//   sum_i g s_{t-1} = P + s_in Q1 + g_out Q2 + s_in g_out R lam^R
+//   P  = sum_i u_i wl_i,  wl_i = lam wl_{i-1} + sl_{i-1}   (wl_{-1} = sl_{-1} = 0)
+//   Q1 = sum_i u_i (i+1) lam^i,  Q2 = lam wl_{R-1}
+//   sum_i gy z' s = sum_i e_i sl_i + s_in sum_i e_i lam^(i+1),  e_i = gy_i d(1/z)/dlam
+// P and the sl/wl terms take one forward sweep over V and gy together; V's
+// registers are free after it.  The g_out terms split into the chunk-local
+// part (known before the look-back) and carry * K, with K summed over the
+// chunk's lanes per channel, so after the look-back one product per channel
+// finishes the chunk's dlam partial.  Only gy is held across the look-back,
+// for the dV pass.  Each chunk writes its dlam partial; the last workgroup of
+// each head sums them in a fixed order (deterministic).
 struct BwdArgs {
   const void* V;
   const void* gy;
@@ -777,19 +827,149 @@ struct ChunkBwd {
   static constexpr int DQ = (DG + 63) / 64;
   static_assert(G + 1 <= NT, "power table is filled one entry per thread");
 
+  // Per row of the chunk (i = the row's index in its lane, 0 <= i < R):
+  // x = 1/z, y = d(1/z)/dlam, z = x (i+1) lam^i + y lam^(i+1), w = x lam^i
+  // (zero for rows past the end).
   struct Smem {
-    float rz[L];       // 1 / z of each row
-    float rzp[L];      // d(1/z)/dlam of each row
+    float4 rt4[L];
     float pw[G + 1];   // lam^(R*k)
+    float pl[R + 1];   // lam^i
     float wt[NW][DG];  // forward per-wavefront totals
     float rt[NW][DG];  // reverse per-wavefront totals
+    float kq[G][DG];   // the carry coefficient K of every lane
     float carry_s[DG]; // state before the chunk's first row
     float carry_g[DG]; // g after the chunk's last row
     float gfin[DG];    // final-state gradient (last chunk only; zero elsewhere)
-    float red[NW];     // dlam partial per wavefront
+    float red[NW];     // carry-free dlam partial per wavefront
   };
 
-  __device__ static void run(const BwdArgs& a, unsigned epoch, Smem& sm) {
+  // Forward sweep over V and gy together (zero state in): sl = lane-local
+  // state, wl = lane-local d(state)/dlam; dq = the sum over the lane's rows
+  // and channels of u wl + e sl, with u = gy / z and e = gy d(1/z)/dlam, taken
+  // per row as rz * sum_j gy wl + rzp * sum_j gy sl.  With GY (few rows per
+  // lane, registers to spare) it also takes sweep_gy's sums, saving that
+  // pass's unpacking.  One row at a time (pin): left free, the compiler ran
+  // the whole state chain first and held every row's states.  Each row's
+  // table entry is read one row ahead.  fin_i: the lane's row N-1
+  // (final-state gradient), or -1.
+  template <bool GY>
+  __device__ static void sweep_fwd(const uint4 (&rv)[R], uint4 (&rg)[R], float lam, int g, int fin_i, int ds,
+                                   const Smem& sm, float (&sl)[VW], float (&wl)[VW], float& dq, float (&qz)[VW],
+                                   float (&ra)[VW]) {
+#pragma unroll
+    for (int j = 0; j < VW; ++j) {
+      sl[j] = 0.0f;
+      wl[j] = 0.0f;
+      if (GY) {
+        qz[j] = 0.0f;
+        ra[j] = 0.0f;
+      }
+    }
+    dq = 0.0f;
+    float2 tz = *reinterpret_cast<const float2*>(&sm.rt4[g * R]);
+    float2 tc = GY ? *reinterpret_cast<const float2*>(&sm.rt4[g * R].z) : make_float2(0.0f, 0.0f);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int in = g * R + (i + 1 < R ? i + 1 : i);
+      const float2 tn = *reinterpret_cast<const float2*>(&sm.rt4[in]);
+      const float2 cn = GY ? *reinterpret_cast<const float2*>(&sm.rt4[in].z) : tc;
+      float v[VW], gv[VW];
+      unpack16<T>(rv[i], v);
+      unpack16<T>(rg[i], gv);
+      float pw = 0.0f, ps = 0.0f;
+#pragma unroll
+      for (int j = 0; j < VW; ++j) {
+        wl[j] = __builtin_fmaf(lam, wl[j], sl[j]);
+        sl[j] = __builtin_fmaf(lam, sl[j], v[j]);
+        pw = __builtin_fmaf(gv[j], wl[j], pw);
+        ps = __builtin_fmaf(gv[j], sl[j], ps);
+        if (GY) {
+          qz[j] = __builtin_fmaf(gv[j], tc.x, qz[j]);
+          ra[j] = __builtin_fmaf(gv[j], tc.y, ra[j]);
+        }
+      }
+      dq = __builtin_fmaf(tz.x, pw, __builtin_fmaf(tz.y, ps, dq));
+      if (i == fin_i) {
+#pragma unroll
+        for (int j = 0; j < VW; ++j) dq = __builtin_fmaf(sm.gfin[ds * VW + j], wl[j], dq);
+      }
+      tz = tn;
+      tc = cn;
+      pin(sl);
+      pin(wl);
+      asm volatile("" : "+v"(dq));
+      if (GY) {
+        pin(qz);
+        pin(ra);
+      }
+    }
+    if (GY) add_fin(fin_i, ds, sm, qz, ra);
+  }
+
+  // The final-state gradient's share of qz and ra (row fin_i of the lane).
+  __device__ static void add_fin(int fin_i, int ds, const Smem& sm, float (&qz)[VW], float (&ra)[VW]) {
+    if (fin_i >= 0) {
+      const float p = sm.pl[fin_i];
+      const float c = p * (float)(fin_i + 1);
+#pragma unroll
+      for (int j = 0; j < VW; ++j) {
+        const float gf = sm.gfin[ds * VW + j];
+        qz[j] = __builtin_fmaf(gf, c, qz[j]);
+        ra[j] = __builtin_fmaf(gf, p, ra[j]);
+      }
+    }
+  }
+
+  // gy-only sweep: qz = Q1 + sum_i e_i lam^(i+1), ra = gl at the lane's first
+  // row (zero carry from the right) = sum_i lam^i u_i.
+  __device__ static void sweep_gy(uint4 (&rg)[R], int g, int fin_i, int ds, const Smem& sm, float (&qz)[VW],
+                                  float (&ra)[VW]) {
+#pragma unroll
+    for (int j = 0; j < VW; ++j) {
+      qz[j] = 0.0f;
+      ra[j] = 0.0f;
+    }
+    float2 tc = *reinterpret_cast<const float2*>(&sm.rt4[g * R].z);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const float2 tn = *reinterpret_cast<const float2*>(&sm.rt4[g * R + (i + 1 < R ? i + 1 : i)].z);
+      float gv[VW];
+      opaque(rg[i]);
+      unpack16<T>(rg[i], gv);
+#pragma unroll
+      for (int j = 0; j < VW; ++j) {
+        qz[j] = __builtin_fmaf(gv[j], tc.x, qz[j]);
+        ra[j] = __builtin_fmaf(gv[j], tc.y, ra[j]);
+      }
+      tc = tn;
+      pin(qz);
+      pin(ra);
+    }
+    add_fin(fin_i, ds, sm, qz, ra);
+  }
+
+  // Reverse pass with the lane's true g_out: g of every row, stored as dV
+  // (rows up to li, the lane's last row inside the sequence).
+  __device__ static void sweep_dv(const BwdArgs& a, uint4 (&rg)[R], float lam, int g, int li, int fin_i, int ds,
+                                  const Smem& sm, T* dp, float (&gn)[VW]) {
+#pragma unroll
+    for (int i = R - 1; i >= 0; --i) {
+      float gv[VW];
+      opaque(rg[i]);
+      unpack16<T>(rg[i], gv);
+      const float rz = sm.rt4[g * R + i].x;
+#pragma unroll
+      for (int j = 0; j < VW; ++j) gn[j] = __builtin_fmaf(lam, gn[j], gv[j] * rz);
+      if (i == fin_i) {
+#pragma unroll
+        for (int j = 0; j < VW; ++j) gn[j] += sm.gfin[ds * VW + j];
+      }
+      if (i <= li) store_vec<T, VW>(dp + (int64_t)i * a.dn, gn);
+      pin(gn);
+    }
+  }
+
+  __device__ static void run(const BwdArgs& a, Smem& sm) {
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const bool multi = a.nchunk > 1;
     const int item = blockIdx.x;
@@ -826,87 +1006,70 @@ struct ChunkBwd {
       if (!fin) cf = 0.0f;
     }
 
-    // Rows of V and gy (rows past the end re-read row N-1; their u is zeroed
-    // and they are left out of every dlam term).
+    // Rows of V and gy, through buffer loads whose range ends with the
+    // stream's row N-1: rows past the end read as zero (the hardware's range
+    // check), so no row index is clamped.  li: index of the lane's last row
+    // inside the sequence (R - 1 outside the last chunk).
+    const int li = a.N - 1 - rbase < R - 1 ? (int)(a.N - 1 - rbase) : R - 1;
     uint4 rv[R], rg[R];
     {
-      const T* vp = static_cast<const T*>(a.V) + b * a.vb + h * a.vh + grp * DG + (int64_t)ds * VW;
-      const T* gp = static_cast<const T*>(a.gy) + b * a.gb + h * a.gh + grp * DG + (int64_t)ds * VW;
+      const __amdgpu_buffer_rsrc_t bv =
+          row_buffer<DG>(static_cast<const T*>(a.V) + b * a.vb + h * a.vh + grp * DG + row0 * a.vn, a.N - row0, a.vn);
+      const __amdgpu_buffer_rsrc_t bg =
+          row_buffer<DG>(static_cast<const T*>(a.gy) + b * a.gb + h * a.gh + grp * DG + row0 * a.gn, a.N - row0, a.gn);
+      const unsigned ov = (unsigned)(((int64_t)g * R * a.vn + ds * VW) * (int64_t)sizeof(T));
+      const unsigned og = (unsigned)(((int64_t)g * R * a.gn + ds * VW) * (int64_t)sizeof(T));
+      const unsigned sv = (unsigned)(a.vn * (int64_t)sizeof(T)), sg = (unsigned)(a.gn * (int64_t)sizeof(T));
+      // Row by row, V then gy: the forward sweep takes them in that order,
+      // as they arrive.
 #pragma unroll
       for (int i = 0; i < R; ++i) {
-        const int64_t r = rbase + i < a.N ? rbase + i : a.N - 1;
-        rv[i] = load16_stream(vp + r * a.vn);
-      }
-#pragma unroll
-      for (int i = 0; i < R; ++i) {
-        const int64_t r = rbase + i < a.N ? rbase + i : a.N - 1;
-        rg[i] = load16_stream(gp + r * a.gn);
+        rv[i] = load16_buffer(bv, ov + i * sv);
+        rg[i] = load16_buffer(bg, og + i * sg);
       }
     }
 
     __syncthreads();
     if (tid <= G) sm.pw[tid] = pow_like_torch(lam, (int64_t)tid * R);
-    // Rows past the end get zeros, so that the passes below read the tables
-    // unconditionally (a read under a condition becomes a branch).
+    if (tid >= NT - (R + 1)) sm.pl[tid - (NT - (R + 1))] = pow_like_torch(lam, (int64_t)(tid - (NT - (R + 1))));
     for (int r = tid; r < L; r += NT) {
       const bool in = row0 + r < a.N;
       const int64_t t = a.t_offset + row0 + r;
-      sm.rz[r] = in ? 1.0f / z_of(lam, t) : 0.0f;
-      sm.rzp[r] = in ? dinvz_dlam(lam, t + 1) : 0.0f;
+      const int i = r % R;
+      const float x = in ? 1.0f / z_of(lam, t) : 0.0f;
+      const float y = in ? dinvz_dlam(lam, t + 1) : 0.0f;
+      const float p = pow_like_torch(lam, i), p1 = p * lam;
+      const float w = x * p;
+      sm.rt4[r] = make_float4(x, y, __builtin_fmaf(w, (float)(i + 1), y * p1), w);
     }
     if (tid < DG) {
       sm.carry_s[tid] = cs;
       sm.gfin[tid] = cf;
     }
+    __syncthreads();  // tables
 
-    // Lane-local forward total of v (zero carry in).
-    float fa[VW];
-#pragma unroll
-    for (int j = 0; j < VW; ++j) fa[j] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-      float v[VW];
-      unpack16<T>(rv[i], v);
-#pragma unroll
-      for (int j = 0; j < VW; ++j) fa[j] = __builtin_fmaf(lam, fa[j], v[j]);
-    }
-    __syncthreads();  // tables, forward carry
+    const int fin_i = rc == 0 && a.gfin != nullptr && li >= 0 && rbase + li == a.N - 1 ? li : -1;
 
-    // u_t = gy_t / z_t (+ the final-state gradient at row N-1) of row i:
-    // branch-free, so that the passes below do not materialise every u.
-    const int fin_i = a.N - 1 >= rbase && a.N - 1 < rbase + R ? (int)(a.N - 1 - rbase) : -1;
-    float gf[VW];
-#pragma unroll
-    for (int j = 0; j < VW; ++j) gf[j] = sm.gfin[ds * VW + j];
-    auto u_of = [&](int i, const float (&gv)[VW], float (&u)[VW]) {
-      const bool valid = rbase + i < a.N;
-      const float rz = sm.rz[g * R + i];
-#pragma unroll
-      for (int j = 0; j < VW; ++j) {
-        const float q = gv[j] * rz;
-        u[j] = i == fin_i ? q + gf[j] : (valid ? q : 0.0f);
-      }
-    };
+    // 16 rows per lane hold 128 registers of rows: there the gy-only sums take
+    // a pass of their own (sweep_gy), so as not to hold 16 more registers
+    // while every row is in flight.
+    constexpr bool kFold = R <= 8;
+    float sl[VW], wl[VW], dq, qz[VW], ra[VW];
+    sweep_fwd<kFold>(rv, rg, lam, g, fin_i, ds, sm, sl, wl, dq, qz, ra);
+    // The launch epoch, first needed to publish (below).  Read here, once
+    // every row has been consumed: loads complete in order, so waiting for it
+    // earlier would have waited for every row (and holding it in a register
+    // across the row loads would spill).
+    const unsigned epoch = read_epoch_v(a.hdr);
+    if (!kFold) sweep_gy(rg, g, fin_i, ds, sm, qz, ra);
 
-    // Lane-local reverse total of u (zero carry from the right).
-    float ra[VW];
-#pragma unroll
-    for (int j = 0; j < VW; ++j) ra[j] = 0.0f;
-#pragma unroll
-    for (int i = R - 1; i >= 0; --i) {
-      float gv[VW], u[VW];
-      unpack16<T>(rg[i], gv);
-      u_of(i, gv, u);
-#pragma unroll
-      for (int j = 0; j < VW; ++j) ra[j] = __builtin_fmaf(lam, ra[j], u[j]);
-    }
-
-    // Scans over the row groups of the wavefront, both directions.
-    group_scan<1, GW, VW, LPR>(fa, gw, sm.pw);
+    // Scans over the row groups of the wavefront, both directions: sl holds
+    // the lane's forward total, ra its reverse total.
+    group_scan<1, GW, VW, LPR>(sl, gw, sm.pw);
     group_scan_rev<1, GW, VW, LPR>(ra, gw, sm.pw);
     if (gw == GW - 1) {
 #pragma unroll
-      for (int j = 0; j < VW; ++j) sm.wt[wave][ds * VW + j] = fa[j];
+      for (int j = 0; j < VW; ++j) sm.wt[wave][ds * VW + j] = sl[j];
     }
     if (gw == 0) {
 #pragma unroll
@@ -915,68 +1078,22 @@ struct ChunkBwd {
     float xin[VW], rin[VW];  // forward: state before the lane; reverse: g after the lane (wave-local)
 #pragma unroll
     for (int j = 0; j < VW; ++j) {
-      const float o = lane_shr<1, GW, LPR>(fa[j]);
+      const float o = lane_shr<1, GW, LPR>(sl[j]);
       xin[j] = gw > 0 ? o : 0.0f;
       const float p = lane_shl<1, GW, LPR>(ra[j]);
       rin[j] = gw < GW - 1 ? p : 0.0f;
     }
     __syncthreads();
 
-    // Forward states of the lane's rows, before the look-back: they depend on
-    // the forward carry only.  s_{t-1} of each row is kept for the dlam term
-    // sum_t g_t s_{t-1}, taken once g is known; sum_t gy_t d(1/z_t)/dlam s_t
-    // is taken here.
+    // Reverse carry of the chunk by look-back over the chunks after it
+    // (wavefront 0, first: later chunks wait on its inclusive word).
     const float mW = sm.pw[GW];
-    const float mg = sm.pw[g], mgw = sm.pw[gw];
-    const float mr = sm.pw[G - 1 - g], mrw = sm.pw[GW - 1 - gw];
-    float gh0[VW];    // g after the lane's last row, zero carry into the chunk's end
-    float sp[R][VW];  // s_{t-1} of the lane's rows
-    float dl = 0.0f;
-    {
-      float ew[VW], er[VW], st[VW];
-#pragma unroll
-      for (int j = 0; j < VW; ++j) {
-        ew[j] = 0.0f;
-        er[j] = 0.0f;
-      }
-      for (int w = 0; w < wave; ++w) {
-#pragma unroll
-        for (int j = 0; j < VW; ++j) ew[j] = __builtin_fmaf(mW, ew[j], sm.wt[w][ds * VW + j]);
-      }
-      for (int w = NW - 1; w > wave; --w) {
-#pragma unroll
-        for (int j = 0; j < VW; ++j) er[j] = __builtin_fmaf(mW, er[j], sm.rt[w][ds * VW + j]);
-      }
-#pragma unroll
-      for (int j = 0; j < VW; ++j) {
-        st[j] = __builtin_fmaf(mg, sm.carry_s[ds * VW + j], __builtin_fmaf(mgw, ew[j], xin[j]));
-        gh0[j] = __builtin_fmaf(mrw, er[j], rin[j]);
-      }
-#pragma unroll
-      for (int i = 0; i < R; ++i) {
-        float v[VW], gv[VW];
-        opaque(rv[i]);
-        opaque(rg[i]);
-        unpack16<T>(rv[i], v);
-        unpack16<T>(rg[i], gv);
-        const bool valid = rbase + i < a.N;
-        const float rzp = sm.rzp[g * R + i];
-#pragma unroll
-        for (int j = 0; j < VW; ++j) {
-          sp[i][j] = st[j];
-          st[j] = __builtin_fmaf(lam, st[j], v[j]);
-          const float t = __builtin_fmaf(gv[j] * rzp, st[j], dl);
-          dl = valid ? t : dl;
-        }
-      }
-    }
-
-    // Reverse carry of the chunk by look-back over the chunks after it.
+    float cg[DQ];
     if (wave == 0) {
       const float mL = sm.pw[G];
       const unsigned tag_agg = tag_of(epoch, 0u), tag_inc = tag_of(epoch, 1u);
       u64* base = multi ? a.flags + (int64_t)stream * a.nchunk * DG : nullptr;
-      float agg[DQ], cg[DQ];
+      float agg[DQ];
 #pragma unroll
       for (int q = 0; q < DQ; ++q) {
         const int d = lane + 64 * q;
@@ -998,7 +1115,63 @@ struct ChunkBwd {
         }
       }
     }
-    __syncthreads();
+
+    // s_in (true, from the saved chunk state) and g_out without the chunk's
+    // carry; the carry-free part of the lane's dlam, and K per channel.
+    const float mg = sm.pw[g], mgw = sm.pw[gw];
+    const float mr = sm.pw[G - 1 - g], mrw = sm.pw[GW - 1 - gw];
+    const float rlr = (float)R * sm.pw[1];
+    float gh0[VW];
+    float dsum = dq;
+    {
+      float ew[VW], er[VW];
+#pragma unroll
+      for (int j = 0; j < VW; ++j) {
+        ew[j] = 0.0f;
+        er[j] = 0.0f;
+      }
+      for (int w = 0; w < wave; ++w) {
+#pragma unroll
+        for (int j = 0; j < VW; ++j) ew[j] = __builtin_fmaf(mW, ew[j], sm.wt[w][ds * VW + j]);
+      }
+      for (int w = NW - 1; w > wave; --w) {
+#pragma unroll
+        for (int j = 0; j < VW; ++j) er[j] = __builtin_fmaf(mW, er[j], sm.rt[w][ds * VW + j]);
+      }
+#pragma unroll
+      for (int j = 0; j < VW; ++j) {
+        const float sin = __builtin_fmaf(mg, sm.carry_s[ds * VW + j], __builtin_fmaf(mgw, ew[j], xin[j]));
+        gh0[j] = __builtin_fmaf(mrw, er[j], rin[j]);
+        const float x = __builtin_fmaf(sin, rlr, lam * wl[j]);  // Q2 + s_in R lam^R
+        dsum = __builtin_fmaf(gh0[j], x, __builtin_fmaf(sin, qz[j], dsum));
+        sm.kq[g][ds * VW + j] = mr * x;
+      }
+    }
+    dsum = wave_sum(dsum);
+    if (lane == 0) sm.red[wave] = dsum;
+    __syncthreads();  // carry_g, kq, red
+
+    // The chunk's dlam partial: the carry-free part plus carry * K.
+    if (wave == 0) {
+      float e = 0.0f;
+#pragma unroll
+      for (int q = 0; q < DQ; ++q) {
+        const int d = lane + 64 * q;
+        if (d < DG) {
+          float kc = 0.0f;
+#pragma unroll
+          for (int r = 0; r < G; ++r) kc += sm.kq[r][d];
+          e = __builtin_fmaf(cg[q], kc, e);
+        }
+      }
+      e = wave_sum(e);
+      if (lane == 0) {
+        float sum = e;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sum += sm.red[w];
+        publish(a.partial + (int64_t)rc * a.nstream + stream, tag_of(epoch, 0u), sum);
+      }
+    }
 
     // Chunk 0 is the last of its stream in this order; see ChunkScan.  (With
     // one chunk per stream every workgroup is a chunk 0: the epoch still
@@ -1011,39 +1184,15 @@ struct ChunkBwd {
       }
     }
 
-    // Reverse pass with the true carry: g of every row, dV, sum_t g_t s_{t-1}.
+    // dV with the true carry.
     float gn[VW];
 #pragma unroll
     for (int j = 0; j < VW; ++j) gn[j] = __builtin_fmaf(mr, sm.carry_g[ds * VW + j], gh0[j]);
     T* dp = static_cast<T*>(a.dv) + b * a.db + h * a.dh + grp * DG + (int64_t)ds * VW + rbase * a.dn;
-#pragma unroll
-    for (int i = R - 1; i >= 0; --i) {
-      float gv[VW], u[VW];
-      opaque(rg[i]);
-      unpack16<T>(rg[i], gv);
-      u_of(i, gv, u);
-      const bool valid = rbase + i < a.N;
-#pragma unroll
-      for (int j = 0; j < VW; ++j) {
-        gn[j] = __builtin_fmaf(lam, gn[j], u[j]);
-        const float t = __builtin_fmaf(gn[j], sp[i][j], dl);
-        dl = valid ? t : dl;
-      }
-      if (valid) store_vec<T, VW>(dp + (int64_t)i * a.dn, gn);
-    }
+    sweep_dv(a, rg, lam, g, li, fin_i, ds, sm, dp, gn);
     if (a.dinit && rbase == 0) {
 #pragma unroll
       for (int j = 0; j < VW; ++j) a.dinit[c0 + ds * VW + j] = lam * gn[j];
-    }
-
-    dl = wave_sum(dl);
-    if (lane == 0) sm.red[wave] = dl;
-    __syncthreads();
-    if (tid == 0) {
-      float sum = 0.0f;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) sum += sm.red[w];
-      publish(a.partial + (int64_t)rc * a.nstream + stream, tag_of(epoch, 0u), sum);
     }
 
     // The workgroup with the largest item index of head h sums the head's
@@ -1094,23 +1243,11 @@ struct ChunkBwd {
   }
 };
 
-// The launch epoch, loaded before the rows like the forward's.  The zero
-// offset comes from a vector register, so the compiler sees a per-lane value
-// and keeps it there: read through a uniform address, the value was moved to
-// a scalar register at once, which waited for the load (and so for a memory
-// round trip) before any row load was issued.
-__device__ __forceinline__ unsigned read_epoch_bwd(const BwdArgs& a) {
-  unsigned zero;
-  asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
-  return __hip_atomic_load(a.hdr + HDR_EPOCH + zero, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-template <typename T, int LPR, int R, int NW, int W>
-__global__ __launch_bounds__(NW * 64) void scan_bwd(BwdArgs a) {
+template <typename T, int LPR, int R, int NW, int W, int WPE>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, 8))) void scan_bwd(BwdArgs a) {
   using CB = ChunkBwd<T, LPR, R, NW, W>;
   __shared__ typename CB::Smem sm;
-  const unsigned epoch = read_epoch_bwd(a);
-  CB::run(a, epoch, sm);
+  CB::run(a, sm);
 }
 
 // --------------------------------------------------------------------------
@@ -1428,35 +1565,54 @@ int dispatch_dg(const ScanArgs& a, int64_t DG, int64_t grid, hipStream_t s, Chun
   return dispatch_dg_r<TI, TO, kR, kNW>(a, DG, grid, s);
 }
 
-// Launch shape of the backward scan: 4 rows per lane (it holds V, gy and g
-// of its rows in registers), 4 wavefronts, a look-back window of 2 (it runs
-// in several rounds; see kWRounds: 2-3% faster than 4 at B=8 N=4096 H=12
-// D=64 bf16, window 1 or 3 slower).
-constexpr int kRB = 4;
+// Launch shape of the backward scan: 4 wavefronts; 16 rows per lane (512-row
+// chunks of a 128-byte channel group: V and gy of the chunk in registers, at
+// most 168 VGPRs for 3 workgroups per CU), or 4 rows per lane when the
+// 16-row grid would leave most of the device idle.  The look-back window is
+// 4 when the whole grid is resident, else 2 (as for the forward).
+constexpr int kRB = 16;
+constexpr int kRBSmall = 4;
 constexpr int kNWB = 4;
-constexpr int kWB = 2;
+constexpr int64_t kBwdSmallGrid = 512;
 
-int64_t bwd_chunk_rows(int v_dtype, int64_t D) {
+int bwd_rows_per_lane(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
+  const int64_t vw = 16 / elem_size(v_dtype);
+  const int64_t DG = group_width(v_dtype, D);
+  const int64_t L = kNWB * (64 / (DG / vw)) * kRB;
+  const int64_t nstream = B * H * (D / DG);
+  return (N + L - 1) / L * nstream <= kBwdSmallGrid ? kRBSmall : kRB;
+}
+
+int64_t bwd_chunk_rows(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   const int64_t vw = 16 / elem_size(v_dtype);
   const int64_t lpr = group_width(v_dtype, D) / vw;
-  return kNWB * (64 / lpr) * kRB;
+  return kNWB * (64 / lpr) * bwd_rows_per_lane(B, H, N, D, v_dtype);
 }
 
 template <typename T, int DG>
-int launch_bwd(const BwdArgs& a, int64_t grid, hipStream_t s) {
+int launch_bwd(const BwdArgs& a, int64_t grid, int R, hipStream_t s) {
   constexpr int VW = 16 / (int)sizeof(T);
   constexpr int LPR = DG / VW;
-  hipLaunchKernelGGL((scan_bwd<T, LPR, kRB, kNWB, kWB>), dim3((unsigned)grid), dim3(kNWB * 64), 0, s, a);
+  if (R == kRB) {
+    auto* const one_round = scan_bwd<T, LPR, kRB, kNWB, kW, 3>;
+    auto* const rounds = scan_bwd<T, LPR, kRB, kNWB, kWRounds, 3>;
+    static const int per_cu = workgroups_per_cu(reinterpret_cast<const void*>(one_round), kNWB * 64);
+    const int64_t resident = (int64_t)per_cu * cu_count();
+    hipLaunchKernelGGL(resident > 0 && grid > resident ? rounds : one_round, dim3((unsigned)grid), dim3(kNWB * 64), 0,
+                       s, a);
+  } else {
+    hipLaunchKernelGGL((scan_bwd<T, LPR, kRBSmall, kNWB, kWRounds, 4>), dim3((unsigned)grid), dim3(kNWB * 64), 0, s, a);
+  }
   return hip_check("scan_bwd launch");
 }
 
 template <typename T>
-int dispatch_bwd(const BwdArgs& a, int64_t DG, int64_t grid, hipStream_t s) {
+int dispatch_bwd(const BwdArgs& a, int64_t DG, int64_t grid, int R, hipStream_t s) {
   switch (DG) {
-    case 16: return launch_bwd<T, 16>(a, grid, s);
-    case 32: return launch_bwd<T, 32>(a, grid, s);
+    case 16: return launch_bwd<T, 16>(a, grid, R, s);
+    case 32: return launch_bwd<T, 32>(a, grid, R, s);
     case 64:
-      if constexpr (sizeof(T) == 2) return launch_bwd<T, 64>(a, grid, s);
+      if constexpr (sizeof(T) == 2) return launch_bwd<T, 64>(a, grid, R, s);
       break;
   }
   return fail(KDECAY_ESHAPE, "unsupported channel group %lld", (long long)DG);
@@ -1629,7 +1785,7 @@ static int scan_fwd_impl(const void* V, int v_dtype, const int64_t* v_strides, v
   a.hdr = need ? static_cast<unsigned*>(workspace) : nullptr;
   a.spin_limit = g_spin_limit;
   a.flags = need ? reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes) : nullptr;
-  a.state_rows = bwd_chunk_rows(v_dtype, D);
+  a.state_rows = bwd_chunk_rows(B, H, N, D, v_dtype);
   a.nsaved = (N + a.state_rows - 1) / a.state_rows;
   a.states = a.nsaved > 1 ? states : nullptr;
 
@@ -1673,7 +1829,7 @@ int kdecay_scan_fwd_noalloc(const void* V, int v_dtype, const int64_t* v_strides
 
 size_t kdecay_scan_saved_states_floats(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   if (B <= 0 || H <= 0 || N <= 0 || !dtype_ok(v_dtype) || !head_dim_ok(v_dtype, D)) return 0;
-  const int64_t Lb = bwd_chunk_rows(v_dtype, D);
+  const int64_t Lb = bwd_chunk_rows(B, H, N, D, v_dtype);
   const int64_t nsaved = (N + Lb - 1) / Lb;
   if (nsaved <= 1) return 0;
   return (size_t)(B * H * D * nsaved);
@@ -1693,7 +1849,7 @@ int kdecay_scan_fwd_train(const void* V, int v_dtype, const int64_t* v_strides, 
 
 size_t kdecay_scan_bwd_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   if (B <= 0 || H <= 0 || N <= 0 || !dtype_ok(v_dtype) || !head_dim_ok(v_dtype, D)) return 0;
-  const int64_t Lb = bwd_chunk_rows(v_dtype, D);
+  const int64_t Lb = bwd_chunk_rows(B, H, N, D, v_dtype);
   const int64_t nchunk = (N + Lb - 1) / Lb;
   const size_t flags = nchunk > 1 ? (size_t)(B * H * nchunk * D) * sizeof(u64) : 0;
   const int64_t nstream = B * H * (D / group_width(v_dtype, D));
@@ -1733,12 +1889,18 @@ int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides, const 
     if (sizes[k] > 1 && (v_strides[k] % vw || gy_strides[k] % vw || dv_strides[k] % vw))
       return fail(KDECAY_ELAYOUT, "stride %d is not a multiple of 16 bytes", k);
   }
-  const int64_t Lb = bwd_chunk_rows(v_dtype, D);
+  const int RB = bwd_rows_per_lane(B, H, N, D, v_dtype);
+  const int64_t Lb = bwd_chunk_rows(B, H, N, D, v_dtype);
   const int64_t nchunk = (N + Lb - 1) / Lb;
   const int64_t DG = group_width(v_dtype, D);
   const int64_t nstream = B * H * (D / DG);
   const int64_t grid = nchunk * nstream;
   if (grid > 0x7fffffffLL) return fail(KDECAY_EINVAL, "problem too large (%lld chunks)", (long long)grid);
+  // The kernel addresses a chunk's rows of V and gy by 32-bit offsets.
+  const int64_t es = elem_size(v_dtype);
+  if (v_strides[2] < 0 || gy_strides[2] < 0) return fail(KDECAY_ELAYOUT, "negative row stride");
+  if (N > 1 && (Lb * v_strides[2] * es > 0x7fffffffLL || Lb * gy_strides[2] * es > 0x7fffffffLL))
+    return fail(KDECAY_ELAYOUT, "row stride too large (%lld rows of a chunk exceed 2^31 bytes)", (long long)Lb);
   if (nchunk > 1 && !states) return fail(KDECAY_EINVAL, "saved states (kdecay_scan_fwd_train) required");
   const size_t need = kdecay_scan_bwd_workspace_bytes(B, H, N, D, v_dtype);
   if (!workspace || workspace_bytes < need)
@@ -1780,11 +1942,11 @@ int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides, const 
   a.partial = reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes + flag_bytes);
   int e;
   if (v_dtype == KDECAY_F32)
-    e = dispatch_bwd<float>(a, DG, grid, s);
+    e = dispatch_bwd<float>(a, DG, grid, RB, s);
   else if (v_dtype == KDECAY_BF16)
-    e = dispatch_bwd<__bf16>(a, DG, grid, s);
+    e = dispatch_bwd<__bf16>(a, DG, grid, RB, s);
   else
-    e = dispatch_bwd<_Float16>(a, DG, grid, s);
+    e = dispatch_bwd<_Float16>(a, DG, grid, RB, s);
   return e;
 }
 

@@ -65,11 +65,15 @@ def test_workspace_bytes(kdecay_lib):
 
 def test_backward_workspace_bytes(kdecay_lib):
     wb = kdecay_lib.kdecay_scan_bwd_workspace_bytes
-    # 128-row chunks (4 rows x 4 wavefronts x 8 row groups for a 128-byte group);
-    # header + look-back words (one per channel per chunk) + one 8-byte tagged
-    # dlam partial per chunk of every stream, rounded up to 256 bytes.
-    nst, nch = 8 * 12, 4096 // 128
+    # 512-row chunks (16 rows x 4 wavefronts x 8 row groups for a 128-byte
+    # group), or 128-row chunks (4 rows) when the 512-row grid has at most 512
+    # chunks; header + look-back words (one per channel per chunk) + one
+    # 8-byte tagged dlam partial per chunk of every stream, rounded up to 256
+    # bytes.
+    nst, nch = 8 * 12, 4096 // 512
     assert wb(8, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    nst, nch = 8 * 6, 1024 // 128  # 96 chunks at 512 rows: the small-grid shape
+    assert wb(8, 6, 1024, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
     # one chunk per stream: no look-back words, but the header and the partials
     assert wb(2, 6, 100, 64, _lib.KDECAY_BF16) == 256 + 256
     assert wb(2, 6, 100, 48, _lib.KDECAY_BF16) == 0  # unsupported D
