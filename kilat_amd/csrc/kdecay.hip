@@ -1573,8 +1573,13 @@ int dispatch_dg(const ScanArgs& a, int64_t DG, int64_t grid, hipStream_t s, Chun
 constexpr int kRB = 16;
 constexpr int kRBSmall = 4;
 constexpr int kNWB = 4;
-constexpr int64_t kBwdSmallGrid = 512;
+constexpr int64_t kBwdSmallGrid = 256;
 
+// 4 rows per lane when the 16-row grid has at most kBwdSmallGrid chunks, so
+// that the 4-row grid (4x the workgroups) still runs in one round; its long
+// chains would otherwise run in several rounds with a narrow window.
+// Measured (bf16 D=64, same-box A/B): B=8 N=1024 H=6 (96 chunks at 16 rows)
+// 4 rows 11.7 us, 16 rows 17.4 us; B=1 N=32768 H=6 (384) 4 rows 84 us.
 int bwd_rows_per_lane(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   const int64_t vw = 16 / elem_size(v_dtype);
   const int64_t DG = group_width(v_dtype, D);
@@ -1594,14 +1599,30 @@ int launch_bwd(const BwdArgs& a, int64_t grid, int R, hipStream_t s) {
   constexpr int VW = 16 / (int)sizeof(T);
   constexpr int LPR = DG / VW;
   if (R == kRB) {
+    // One round: window 4, or 8 for chains of more than 8 chunks (a window
+    // of 16 does not fit beside 16 rows per lane without spilling); several
+    // rounds: 2.
     auto* const one_round = scan_bwd<T, LPR, kRB, kNWB, kW, 3>;
-    auto* const rounds = scan_bwd<T, LPR, kRB, kNWB, kWRounds, 3>;
     static const int per_cu = workgroups_per_cu(reinterpret_cast<const void*>(one_round), kNWB * 64);
     const int64_t resident = (int64_t)per_cu * cu_count();
-    hipLaunchKernelGGL(resident > 0 && grid > resident ? rounds : one_round, dim3((unsigned)grid), dim3(kNWB * 64), 0,
-                       s, a);
+    auto* const k = resident > 0 && grid > resident ? scan_bwd<T, LPR, kRB, kNWB, kWRounds, 3>
+                    : a.nchunk > 8                  ? scan_bwd<T, LPR, kRB, kNWB, 8, 3>
+                                                    : one_round;
+    hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(kNWB * 64), 0, s, a);
   } else {
-    hipLaunchKernelGGL((scan_bwd<T, LPR, kRBSmall, kNWB, kWRounds, 4>), dim3((unsigned)grid), dim3(kNWB * 64), 0, s, a);
+    // Small grids: by chain length when the grid is resident, as for the
+    // forward's small grids.  Measured (bf16 D=64, same-box A/B, window 2 /
+    // 4 / 8): B=8 N=1024 H=6 (8 chunks per stream) 12.13 / 11.73 / 11.94 us;
+    // B=2 N=4096 H=12 (32) 19.65 / 15.73 / 14.90 us; B=1 N=8192 H=6 (64)
+    // 28.11 / 20.45 / 16.34 us.
+    auto* const w4 = scan_bwd<T, LPR, kRBSmall, kNWB, 4, 4>;
+    static const int per_cu = workgroups_per_cu(reinterpret_cast<const void*>(w4), kNWB * 64);
+    const int64_t resident = (int64_t)per_cu * cu_count();
+    auto* const k = resident > 0 && grid > resident ? scan_bwd<T, LPR, kRBSmall, kNWB, kWRounds, 4>
+                    : a.nchunk > 32                 ? scan_bwd<T, LPR, kRBSmall, kNWB, 16, 4>
+                    : a.nchunk > 8                  ? scan_bwd<T, LPR, kRBSmall, kNWB, 8, 4>
+                                                    : w4;
+    hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(kNWB * 64), 0, s, a);
   }
   return hip_check("scan_bwd launch");
 }
