@@ -80,10 +80,10 @@ def test_backward_shapes(hip_device, kdecay_lib, dname, D):
 
 @pytest.mark.parametrize("dname,H,D", [("f32", 4, 64), ("bf16", 2, 128)])
 def test_backward_long_sequence(hip_device, kdecay_lib, dname, H, D):
-    """N = 65536: 512 backward chunks per stream, so the reverse look-back
-    runs 512 chunks deep and each head's dlam sums 1024 chunk partials (two
-    rounds of the reducing wavefront's reads), against the fp64 adjoint
-    recurrence (oracle.decay_oracle.scan_grads_f64)."""
+    """N = 65536: 128 backward chunks of 512 rows per stream, so the reverse
+    look-back runs 128 chunks deep (several rounds for f32, one round with
+    the window of 8 for bf16) and each head's dlam sums 256 chunk partials,
+    against the fp64 adjoint recurrence (oracle.decay_oracle.scan_grads_f64)."""
     dtype = DTYPES[dname]
     g = torch.Generator().manual_seed(210 + D)
     lam = lam_uniform(H, 0.9, 0.9999, g)
@@ -141,9 +141,8 @@ def test_backward_give_up_is_flagged_not_hung(hip_device, kdecay_lib):
 def test_backward_randomized(hip_device, kdecay_lib):
     """A seeded sweep of 24 random backward cases against the fp64 adjoint
     recurrence: dtypes, head dims, grids on both sides of the forward's
-    small-grid limit, lengths around the 128-row backward chunks, decay
-    factors from 0.3 to 0.9999, with or without carry-in, final-state
-    gradient and offset."""
+    small-grid limit, lengths around 128-row chunks, decay factors from 0.3
+    to 0.9999, with or without carry-in, final-state gradient and offset."""
     import numpy as np
 
     rng = np.random.default_rng(4048)
@@ -355,3 +354,28 @@ def test_backward_sequential_and_out(hip_device, kdecay_lib, D):
         (y * gy.to(hip_device)).sum().backward()
         torch.cuda.synchronize()
         check(V_d.grad.cpu(), lam_d.grad.cpu(), None, rdv, rdl, None, torch.float32, f"D={D} {list(kw)}")
+
+
+@pytest.mark.parametrize("B,N", [(8, 2600), (2, 700)])
+def test_backward_layout_fused_and_broadcast_gradient(hip_device, kdecay_lib, B, N):
+    """V as the attention's projection output [B,N,H*D] viewed as [B,H,N,D]
+    (row stride H*D, no copy) and the loss y.sum(), whose upstream gradient
+    is a broadcast tensor of ones (every stride 0): the 512-row backward
+    (B=8: 384 chunks, the tail chunk 40 rows long) and the 128-row one (B=2),
+    against the fp64 adjoint recurrence."""
+    H, D = 8, 64
+    g = torch.Generator().manual_seed(214 + B)
+    lam = lam_uniform(H, 0.8, 0.9999, g)
+    proj = torch.randn(B, N, H * D, generator=g).to(torch.bfloat16)
+    P = proj.to(hip_device).requires_grad_(True)
+    Vd = P.view(B, N, H, D).transpose(1, 2)
+    assert Vd.stride(2) == H * D
+    lam_d = lam.to(hip_device).requires_grad_(True)
+    print(f"  fused-layout grad B={B} N={N}", flush=True)
+    y = kilat_amd.global_decay_scan(lam_d, Vd)
+    y.sum().backward()
+    torch.cuda.synchronize()
+    V = proj.view(B, N, H, D).transpose(1, 2).contiguous()
+    rdv, rdl, _ = O.scan_grads_f64(lam, V, torch.ones(B, H, N, D, dtype=torch.float64))
+    dv = P.grad.cpu().view(B, N, H, D).transpose(1, 2)
+    check(dv, lam_d.grad.cpu(), None, rdv, rdl, None, torch.bfloat16, f"fused layout B={B} N={N}")
