@@ -258,6 +258,14 @@ const char* kdecay_last_error_string(void);
  */
 int kdecay_debug_set_spin_limit(int polls);
 
+/*
+ * Test hook, no counterpart in the reference: the quotient n / d (want_mod
+ * == 0) or remainder n % d as the kernels compute it, by the multiply and
+ * shift the library derives for d on the host (valid for 0 <= n < 2^31,
+ * 1 <= d < 2^31), so a CPU test can check it against exact division.
+ */
+uint32_t kdecay_debug_fastdiv(uint32_t n, uint32_t d, int want_mod);
+
 #ifdef __cplusplus
 }
 #endif

@@ -41,6 +41,7 @@ EXPORTS = (
     "kdecay_version",
     "kdecay_last_error_string",
     "kdecay_debug_set_spin_limit",
+    "kdecay_debug_fastdiv",
 )
 
 _c_i64 = ctypes.c_int64
@@ -132,6 +133,8 @@ def load() -> ctypes.CDLL:
     lib.kdecay_last_error_string.argtypes = []
     lib.kdecay_debug_set_spin_limit.restype = ctypes.c_int
     lib.kdecay_debug_set_spin_limit.argtypes = [ctypes.c_int]
+    lib.kdecay_debug_fastdiv.restype = ctypes.c_uint32
+    lib.kdecay_debug_fastdiv.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int]
     _lib = lib
     return lib
 

@@ -199,6 +199,30 @@ __device__ __forceinline__ float z_of_fast(float lam, int64_t t) {
 }
 
 // --------------------------------------------------------------------------
+// Division by a divisor fixed for the launch: a multiply and a shift
+// (Granlund & Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994, theorem 4.2 with N = 31: for 2^(l-1) < d <= 2^l
+// and m = ceil(2^(31+l) / d) < 2^32, floor(n * m / 2^(31+l)) = floor(n / d)
+// for 0 <= n < 2^31).  A compiled division by a runtime value is a chain of
+// about 25 dependent instructions (a 64-bit one about 100); the kernels do
+// theirs before their first load.
+// --------------------------------------------------------------------------
+struct FastDiv {
+  uint32_t d, m, s;
+  __host__ __device__ uint32_t div(uint32_t n) const { return (uint32_t)(((uint64_t)n * m) >> s); }
+  __host__ __device__ uint32_t mod(uint32_t n) const { return n - div(n) * d; }
+};
+
+// d >= 1.
+inline FastDiv make_fastdiv(uint32_t d) {
+  uint32_t l = 0;
+  while (l < 32 && ((uint64_t)1 << l) < d) ++l;
+  const uint32_t s = 31 + l;
+  const uint64_t p = (uint64_t)1 << s;  // s <= 63
+  return FastDiv{d, (uint32_t)((p + d - 1) / d), s};
+}
+
+// --------------------------------------------------------------------------
 // Look-back words and the workspace header
 // --------------------------------------------------------------------------
 typedef unsigned long long u64;
@@ -412,6 +436,7 @@ struct ScanArgs {
   int64_t state_rows;
   int64_t nsaved;
   int spin_limit;  // polls before a look-back gives up (kSpinLimit unless a test lowers it)
+  FastDiv f_nstream, f_ng, f_H;  // division by nstream, ng and H
 };
 
 // 16-byte load of data read exactly once (non-temporal: no cache residency).
@@ -477,6 +502,24 @@ __device__ __forceinline__ int rotated_stream(int j, int rot, int nstream) {
   return k >= nstream ? k - nstream : k;
 }
 
+// Where item `item` of a launch is: chunk (row of chunks), stream, and the
+// stream's (b, h, channel group).  Computed once per workgroup.
+struct Pos {
+  int chunk, stream, bh, grp, b, h;
+};
+
+__device__ __forceinline__ Pos pos_of(const ScanArgs& a, int item) {
+  Pos p;
+  p.chunk = (int)a.f_nstream.div((uint32_t)item);
+  const int j = item - p.chunk * a.nstream;
+  p.stream = rotated_stream(j, (int)a.f_nstream.mod((uint32_t)p.chunk), a.nstream);
+  p.bh = (int)a.f_ng.div((uint32_t)p.stream);
+  p.grp = p.stream - p.bh * a.ng;
+  p.b = (int)a.f_H.div((uint32_t)p.bh);
+  p.h = p.bh - p.b * (int)a.H;
+  return p;
+}
+
 // One chunk ("item") of the scan: L rows x DG channels of one stream.  A
 // stream is one (b,h) pair and one group of DG channels, at most 128 bytes of
 // each row: wider heads are split into independent channel groups, which
@@ -525,11 +568,10 @@ struct ChunkScan {
   // look-back's join whether the load was still pending, and it waited there
   // for every memory operation, the chunk's own look-back publishes included
   // (a device-scope store round trip on every chunk's critical path).
-  __device__ static float load(const ScanArgs& a, int item, uint4 (&raw)[R], float& init) {
+  __device__ static float load(const ScanArgs& a, const Pos& p, uint4 (&raw)[R], float& init) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int chunk = item / a.nstream, stream = rotated_stream(item % a.nstream, chunk % a.nstream, a.nstream);
-    const int64_t bh = stream / a.ng, grp = stream % a.ng;
-    const int64_t b = bh / a.H, h = bh % a.H;
+    const int chunk = p.chunk;
+    const int64_t bh = p.bh, grp = p.grp, b = p.b, h = p.h;
     const float lam = a.lam[h];
     {
       const bool has = chunk == 0 && a.init != nullptr;
@@ -552,12 +594,12 @@ struct ChunkScan {
   // launch generation every workgroup read before publishing anything.
   // Tables, chunk reduction and look-back: st = the state before this lane's
   // first row.
-  __device__ static void scan_chunk(const ScanArgs& a, int item, uint4 (&raw)[R], float lam, float init,
+  __device__ static void scan_chunk(const ScanArgs& a, const Pos& p, uint4 (&raw)[R], float lam, float init,
                                     unsigned epoch, Smem& sm, float (&st)[VW]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const bool multi = a.nchunk > 1;
-    const int chunk = item / a.nstream, stream = rotated_stream(item % a.nstream, chunk % a.nstream, a.nstream);
-    const int64_t bh = stream / a.ng, grp = stream % a.ng;
+    const int chunk = p.chunk, stream = p.stream;
+    const int64_t bh = p.bh, grp = p.grp;
     const int64_t c0 = bh * a.D + grp * DG;  // channel 0 of this stream in [B*H*D] state arrays
     const int64_t row0 = (int64_t)chunk * L;
     const bool last = chunk == a.nchunk - 1;
@@ -658,12 +700,11 @@ struct ChunkScan {
   }
 
   // Re-run the lane's rows from st and store y (and the optional outputs).
-  __device__ static void store_chunk(const ScanArgs& a, int item, uint4 (&raw)[R], float lam, float (&st)[VW],
+  __device__ static void store_chunk(const ScanArgs& a, const Pos& p, uint4 (&raw)[R], float lam, float (&st)[VW],
                                      const Smem& sm) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int chunk = item / a.nstream, stream = rotated_stream(item % a.nstream, chunk % a.nstream, a.nstream);
-    const int bh = stream / a.ng, grp = stream % a.ng;
-    const int b = bh / (int)a.H, h = bh % (int)a.H;  // 32-bit: bh < nstream
+    const int chunk = p.chunk, stream = p.stream;
+    const int bh = p.bh, grp = p.grp, b = p.b, h = p.h;
     const int64_t c0 = (int64_t)bh * a.D + grp * DG;
     const int ds = lane % LPR, gw = lane / LPR;
     const int g = wave * GW + gw;
@@ -703,11 +744,11 @@ struct ChunkScan {
     }
   }
 
-  __device__ static void process(const ScanArgs& a, int item, uint4 (&raw)[R], float lam, float init,
+  __device__ static void process(const ScanArgs& a, const Pos& p, uint4 (&raw)[R], float lam, float init,
                                  unsigned epoch, Smem& sm) {
     float st[VW];
-    scan_chunk(a, item, raw, lam, init, epoch, sm, st);
-    store_chunk(a, item, raw, lam, st, sm);
+    scan_chunk(a, p, raw, lam, init, epoch, sm, st);
+    store_chunk(a, p, raw, lam, st, sm);
   }
 };
 
@@ -728,10 +769,11 @@ void scan_chunked(ScanArgs a) {
   using CS = ChunkScan<TI, TO, LPR, R, NW, W, FZ>;
   __shared__ typename CS::Smem sm;
   const unsigned epoch = read_epoch(a);
+  const Pos p = pos_of(a, (int)blockIdx.x);
   uint4 raw[R];
   float init;
-  const float lam = CS::load(a, blockIdx.x, raw, init);
-  CS::process(a, blockIdx.x, raw, lam, init, epoch, sm);
+  const float lam = CS::load(a, p, raw, init);
+  CS::process(a, p, raw, lam, init, epoch, sm);
 }
 
 // --------------------------------------------------------------------------
@@ -780,6 +822,7 @@ struct BwdArgs {
   u64* flags;
   unsigned* hdr;
   int spin_limit;  // as ScanArgs::spin_limit, for the look-back and the dlam reduction
+  FastDiv f_nstream, f_ng, f_H, f_nchunk;  // division by nstream, ng, H and nchunk
 };
 
 // d(1/z)/dlam for z = (1 - lam^e) / ((1 - lam) + 1e-6), evaluated in double.
@@ -975,11 +1018,11 @@ struct ChunkBwd {
     const int item = blockIdx.x;
     // rc: position from the end.  The rotation leaves the last row (rc =
     // nchunk-1) unrotated, which reduce_head's choice of workgroup relies on.
-    const int rc = item / a.nstream;
-    const int stream = rotated_stream(item % a.nstream, (a.nchunk - 1 - rc) % a.nstream, a.nstream);
+    const int rc = (int)a.f_nstream.div((uint32_t)item);
     const int chunk = a.nchunk - 1 - rc;
-    const int bh = stream / a.ng, grp = stream % a.ng;
-    const int b = bh / (int)a.H, h = bh % (int)a.H;  // 32-bit: bh < nstream
+    const int stream = rotated_stream(item - rc * a.nstream, (int)a.f_nstream.mod((uint32_t)chunk), a.nstream);
+    const int bh = (int)a.f_ng.div((uint32_t)stream), grp = stream - bh * a.ng;
+    const int b = (int)a.f_H.div((uint32_t)bh), h = bh - b * (int)a.H;
     const int64_t c0 = (int64_t)bh * a.D + grp * DG;
     const int64_t row0 = (int64_t)chunk * L;
     const int ds = lane % LPR, gw = lane / LPR;
@@ -1218,8 +1261,8 @@ struct ChunkBwd {
 #pragma unroll
       for (int k = 0; k < K; ++k) {
         const int idx = i0 + lane + 64 * k < n ? i0 + lane + 64 * k : n - 1;
-        const int rc = idx % a.nchunk, bg = idx / a.nchunk;
-        const int b = bg / a.ng, grp = bg % a.ng;
+        const int bg = (int)a.f_nchunk.div((uint32_t)idx), rc = idx - bg * a.nchunk;
+        const int b = (int)a.f_ng.div((uint32_t)bg), grp = bg - b * a.ng;
         p[k] = a.partial + (int64_t)rc * a.nstream + ((int64_t)b * a.H + h) * a.ng + grp;
         w[k] = peek(p[k]);
       }
@@ -1294,6 +1337,7 @@ struct StepArgs {
   const int32_t* tpos;
   int64_t tpos_scalar;
   int64_t H, D, total;
+  FastDiv f_D, f_H;  // division by D and H (the four-wide kernel)
 };
 
 template <typename TV, typename TO>
@@ -1352,8 +1396,8 @@ __global__ __launch_bounds__(256) void decay_step4(StepArgs a) {
   // 32-bit indices: the host launches this kernel only when total < 2^31.
   const int idx = (int)(blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (idx >= (int)a.total) return;
-  const int bh = idx / (int)a.D;
-  const int h = bh % (int)a.H, b = bh / (int)a.H;
+  const int bh = (int)a.f_D.div((uint32_t)idx);
+  const int b = (int)a.f_H.div((uint32_t)bh), h = bh - b * (int)a.H;
   // The decay factor and position first (z needs them first, and memory
   // operations complete in issue order), then the state and v.  The position
   // load is unconditional (a load under a branch is waited for at the branch
@@ -1740,6 +1784,12 @@ int kdecay_debug_set_spin_limit(int polls) {
   return previous == kSpinLimit ? 0 : previous;
 }
 
+uint32_t kdecay_debug_fastdiv(uint32_t n, uint32_t d, int want_mod) {
+  if (d == 0) return 0;
+  const FastDiv f = make_fastdiv(d);
+  return want_mod ? f.mod(n) : f.div(n);
+}
+
 size_t kdecay_scan_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   if (B <= 0 || H <= 0 || N <= 0 || !dtype_ok(v_dtype) || !head_dim_ok(v_dtype, D)) return 0;
   const int64_t L = chunk_rows(v_dtype, D, chunk_shape(B, H, N, D, v_dtype));
@@ -1803,6 +1853,9 @@ static int scan_fwd_impl(const void* V, int v_dtype, const int64_t* v_strides, v
   a.ng = (int)(D / DG);
   a.nchunk = (int)nchunk;
   a.nstream = (int)nstream;
+  a.f_nstream = make_fastdiv((uint32_t)nstream);
+  a.f_ng = make_fastdiv((uint32_t)a.ng);
+  a.f_H = make_fastdiv((uint32_t)H);
   a.hdr = need ? static_cast<unsigned*>(workspace) : nullptr;
   a.spin_limit = g_spin_limit;
   a.flags = need ? reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes) : nullptr;
@@ -1956,6 +2009,10 @@ int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides, const 
   a.nchunk = (int)nchunk;
   a.nstream = (int)nstream;
   a.nsaved = nchunk;
+  a.f_nstream = make_fastdiv((uint32_t)nstream);
+  a.f_ng = make_fastdiv((uint32_t)a.ng);
+  a.f_H = make_fastdiv((uint32_t)H);
+  a.f_nchunk = make_fastdiv((uint32_t)nchunk);
   a.hdr = static_cast<unsigned*>(workspace);
   a.spin_limit = g_spin_limit;
   const size_t flag_bytes = nchunk > 1 ? (size_t)(B * H * nchunk * D) * sizeof(u64) : 0;
@@ -2027,6 +2084,8 @@ int kdecay_step(const float* lam, const float* state_in, const void* v_t, int v_
   a.H = H;
   a.D = D;
   a.total = total;
+  a.f_D = make_fastdiv((uint32_t)D);
+  a.f_H = make_fastdiv((uint32_t)H);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (v_dtype * 3 + out_dtype) {
     case KDECAY_F32 * 3 + KDECAY_F32: return launch_step<float, float>(a, s);

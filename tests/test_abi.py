@@ -173,7 +173,7 @@ def test_ctypes_signatures_cover_header(kdecay_lib):
     # every declared function has an explicit restype (a missing one would
     # silently truncate size_t / pointer returns to int)
     for sym in declared_symbols():
-        assert getattr(kdecay_lib, sym).restype in (ctypes.c_int, ctypes.c_size_t, ctypes.c_char_p), sym
+        assert getattr(kdecay_lib, sym).restype in (ctypes.c_int, ctypes.c_uint32, ctypes.c_size_t, ctypes.c_char_p), sym
 
 
 def test_integration_patches_every_module_by_name():
@@ -247,3 +247,25 @@ def test_library_takes_the_same_head_dims(kdecay_lib):
         for D in range(1, 400):
             ok = kdecay_lib.kdecay_scan_workspace_bytes(2, 3, 100000, D, code) > 0
             assert ok == chunked_head_dim(D, dt), (dt, D)
+
+
+def test_fast_division_matches_exact_division(kdecay_lib):
+    """The kernels divide by launch-invariant integers (streams, channel
+    groups, heads, head dims, chunks) with a multiply and a shift derived on
+    the host; the same host code answers kdecay_debug_fastdiv.  Checked
+    against exact division for every divisor up to 4096 at edge and random
+    dividends, and for large and power-of-two divisors up to 2^31 - 1."""
+    import numpy as np
+
+    fd = kdecay_lib.kdecay_debug_fastdiv
+    rng = np.random.default_rng(7)
+    top = (1 << 31) - 1
+    divisors = list(range(1, 4097)) + [int(x) for x in rng.integers(4097, top, 400)]
+    divisors += [1 << k for k in range(31)] + [(1 << k) + 1 for k in range(1, 31)] + [(1 << k) - 1 for k in range(2, 32)]
+    for d in divisors:
+        ns = {0, 1, d - 1, d, d + 1, 2 * d - 1, top, top - 1, top - d, (top // d) * d, (top // d) * d - 1}
+        ns.update(int(x) for x in rng.integers(0, top, 8))
+        for n in ns:
+            if 0 <= n <= top:
+                assert fd(n, d, 0) == n // d, (n, d)
+                assert fd(n, d, 1) == n % d, (n, d)
