@@ -190,7 +190,11 @@ size_t kdecay_scan_saved_states_floats(int64_t B, int64_t H, int64_t N,
  * with s the forward states (s_{-1} = init_state or 0).
  *
  *   V, gy, dV    [B,H,N,D] of v_dtype (gy and dV share V's dtype), strided as
- *                kdecay_scan_fwd's V
+ *                kdecay_scan_fwd's V; the row strides of V and gy must not
+ *                be negative, and one backward chunk of rows (512 rows, or
+ *                128 for grids of at most 256 such chunks) must span less
+ *                than 2^31 bytes (rows are addressed by 32-bit offsets), else
+ *                KDECAY_ELAYOUT
  *   lam, init_state, t_offset   as given to the forward call
  *   states       the forward call's states (NULL allowed when
  *                kdecay_scan_saved_states_floats() is 0)
