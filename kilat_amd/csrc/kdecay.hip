@@ -1027,7 +1027,7 @@ struct ChunkBwd {
     const int64_t row0 = (int64_t)chunk * L;
     const int ds = lane % LPR, gw = lane / LPR;
     const int g = wave * GW + gw;
-    const int64_t rbase = row0 + (int64_t)g * R;
+    const int gr = g * R;  // the lane's first row within the chunk (rows row0 + gr ...)
     const float lam = a.lam[h];
 
     // For channel tid < DG: the forward state before the chunk's first row
@@ -1053,7 +1053,8 @@ struct ChunkBwd {
     // stream's row N-1: rows past the end read as zero (the hardware's range
     // check), so no row index is clamped.  li: index of the lane's last row
     // inside the sequence (R - 1 outside the last chunk).
-    const int li = a.N - 1 - rbase < R - 1 ? (int)(a.N - 1 - rbase) : R - 1;
+    const int64_t left = a.N - 1 - row0;  // the chunk's last row inside the sequence
+    const int li = left - gr < R - 1 ? (int)(left - gr) : R - 1;
     uint4 rv[R], rg[R];
     {
       const __amdgpu_buffer_rsrc_t bv =
@@ -1091,7 +1092,7 @@ struct ChunkBwd {
     }
     __syncthreads();  // tables
 
-    const int fin_i = rc == 0 && a.gfin != nullptr && li >= 0 && rbase + li == a.N - 1 ? li : -1;
+    const int fin_i = rc == 0 && a.gfin != nullptr && li >= 0 && gr + li == left ? li : -1;
 
     // 16 rows per lane hold 128 registers of rows: there the gy-only sums take
     // a pass of their own (sweep_gy), so as not to hold 16 more registers
@@ -1231,9 +1232,9 @@ struct ChunkBwd {
     float gn[VW];
 #pragma unroll
     for (int j = 0; j < VW; ++j) gn[j] = __builtin_fmaf(mr, sm.carry_g[ds * VW + j], gh0[j]);
-    T* dp = static_cast<T*>(a.dv) + b * a.db + h * a.dh + grp * DG + (int64_t)ds * VW + rbase * a.dn;
+    T* dp = static_cast<T*>(a.dv) + b * a.db + h * a.dh + grp * DG + row0 * a.dn + ((int64_t)gr * a.dn + ds * VW);
     sweep_dv(a, rg, lam, g, li, fin_i, ds, sm, dp, gn);
-    if (a.dinit && rbase == 0) {
+    if (a.dinit && row0 + gr == 0) {
 #pragma unroll
       for (int j = 0; j < VW; ++j) a.dinit[c0 + ds * VW + j] = lam * gn[j];
     }
