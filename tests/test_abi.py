@@ -106,6 +106,39 @@ def test_scan_rejects_bad_arguments(kdecay_lib):
     assert rc == _lib.KDECAY_EINVAL
 
 
+def _bwd(lib, N=4096, D=64, vstr=None, gstr=None, V=FAKE, states=FAKE, ws=FAKE, wsb=1 << 30):
+    B, H = 8, 12  # 768 chunks of 512 rows
+    vstr = vstr or (H * N * D, N * D, D, 1)
+    gstr = gstr or (H * N * D, N * D, D, 1)
+    dstr = (H * N * D, N * D, D, 1)
+    return lib.kdecay_scan_bwd(V, _lib.KDECAY_BF16, _lib.strides4(vstr), FAKE, _lib.strides4(gstr), FAKE,
+                               _lib.strides4(dstr), FAKE, None, states, None, FAKE, None, B, H, N, D, 0,
+                               ws, wsb, None)
+
+
+def test_backward_rejects_bad_arguments(kdecay_lib):
+    """The backward's checks run before any HIP call.  Its rows are read
+    through 32-bit buffer offsets from each chunk's first row, so a row stride
+    at which one chunk (512 rows here) spans 2^31 bytes or more, and a
+    negative row stride, are refused with KDECAY_ELAYOUT."""
+    lib = kdecay_lib
+    H, N, D = 12, 4096, 64
+    assert _bwd(lib, D=48) == _lib.KDECAY_ESHAPE
+    assert _bwd(lib, V=FAKE + 2) == _lib.KDECAY_ELAYOUT
+    assert _bwd(lib, vstr=(H * N * D, N * D, -D, 1)) == _lib.KDECAY_ELAYOUT
+    assert "negative row stride" in lib.kdecay_last_error_string().decode()
+    # 512 rows x 2 bytes x stride: 2^21 elements reach 2^31 bytes, 2^21 - 64 stay below
+    big = 1 << 21
+    assert _bwd(lib, gstr=(H * N * big, N * big, big, 1)) == _lib.KDECAY_ELAYOUT
+    assert "2^31" in lib.kdecay_last_error_string().decode()
+    assert _bwd(lib, vstr=(H * N * big, N * big, big, 1)) == _lib.KDECAY_ELAYOUT
+    ok = big - 64
+    assert _bwd(lib, vstr=(H * N * ok, N * ok, ok, 1), ws=None, wsb=0) == _lib.KDECAY_EWORKSPACE
+    assert _bwd(lib, states=None) == _lib.KDECAY_EINVAL  # several chunks need the saved states
+    assert _bwd(lib, ws=None, wsb=0) == _lib.KDECAY_EWORKSPACE
+    assert _bwd(lib, ws=FAKE + 16) == _lib.KDECAY_EWORKSPACE  # not 256-byte aligned
+
+
 def test_noalloc_scan_rejects_oversized_and_bad_arguments(kdecay_lib):
     """The allocation-free entry point checks its arguments, and that the
     shape's workspace fits its fixed device array, before it touches the
