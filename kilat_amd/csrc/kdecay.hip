@@ -1659,12 +1659,15 @@ int launch_bwd(const BwdArgs& a, int64_t grid, int R, hipStream_t s) {
     // forward's small grids.  Measured (bf16 D=64, same-box A/B, window 2 /
     // 4 / 8): B=8 N=1024 H=6 (8 chunks per stream) 12.13 / 11.73 / 11.94 us;
     // B=2 N=4096 H=12 (32) 19.65 / 15.73 / 14.90 us; B=1 N=8192 H=6 (64)
-    // 28.11 / 20.45 / 16.34 us.
+    // 28.11 / 20.45 / 16.34 us.  The window-16 kernel holds 32 registers of
+    // look-back words: within 128 VGPRs (4 waves per SIMD) it spilled 20-24
+    // bytes, so it is built for 3 waves per SIMD (B=1 N=16384 H=6 20.1 ->
+    // 18.4 us, B=1 N=65536 H=2 43.1 -> 39.7 us, same-box A/B).
     auto* const w4 = scan_bwd<T, LPR, kRBSmall, kNWB, 4, 4>;
     static const int per_cu = workgroups_per_cu(reinterpret_cast<const void*>(w4), kNWB * 64);
     const int64_t resident = (int64_t)per_cu * cu_count();
     auto* const k = resident > 0 && grid > resident ? scan_bwd<T, LPR, kRBSmall, kNWB, kWRounds, 4>
-                    : a.nchunk > 32                 ? scan_bwd<T, LPR, kRBSmall, kNWB, 16, 4>
+                    : a.nchunk > 32                 ? scan_bwd<T, LPR, kRBSmall, kNWB, 16, 3>
                     : a.nchunk > 8                  ? scan_bwd<T, LPR, kRBSmall, kNWB, 8, 4>
                                                     : w4;
     hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(kNWB * 64), 0, s, a);

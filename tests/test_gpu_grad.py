@@ -78,12 +78,14 @@ def test_backward_shapes(hip_device, kdecay_lib, dname, D):
         check(dv, dl, None, rdv, rdl, None, dtype, f"D={D} N={N}")
 
 
-@pytest.mark.parametrize("dname,H,D", [("f32", 4, 64), ("bf16", 2, 128)])
+@pytest.mark.parametrize("dname,H,D", [("f32", 4, 64), ("bf16", 2, 128), ("bf16", 2, 64)])
 def test_backward_long_sequence(hip_device, kdecay_lib, dname, H, D):
     """N = 65536: 128 backward chunks of 512 rows per stream, so the reverse
     look-back runs 128 chunks deep (several rounds for f32, one round with
-    the window of 8 for bf16) and each head's dlam sums 256 chunk partials,
-    against the fp64 adjoint recurrence (oracle.decay_oracle.scan_grads_f64)."""
+    the window of 8 for bf16 D=128) and each head's dlam sums 256 chunk
+    partials; bf16 H=2 D=64 (a 256-chunk grid at 512 rows) takes 128-row
+    chunks instead, 512 per stream, with the window of 16.  Against the fp64
+    adjoint recurrence (oracle.decay_oracle.scan_grads_f64)."""
     dtype = DTYPES[dname]
     g = torch.Generator().manual_seed(210 + D)
     lam = lam_uniform(H, 0.9, 0.9999, g)
