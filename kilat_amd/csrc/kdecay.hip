@@ -159,6 +159,14 @@ __device__ __forceinline__ float pow_like_torch(float x, int64_t e) {
   return (float)ipow_f64((double)x, e);
 }
 
+// Wait until at most N vector memory operations of this wavefront are
+// outstanding (vmcnt only; the other counters are left alone).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 __device__ __forceinline__ float z_of(float lam, int64_t t) {
   const float num = 1.0f - pow_like_torch(lam, t + 1);
   const float den = (1.0f - lam) + 1e-6f;
@@ -527,12 +535,13 @@ __device__ __forceinline__ Pos pos_of(const ScanArgs& a, int item) {
 // streams and shorter look-back chains.
 // TI/TO: element types of V / out.  LPR lanes cover one row slice (DG = LPR * VW);
 // each lane owns R consecutive rows of one 16-byte channel slice; NW
-// wavefronts per workgroup; W = look-back window.
+// wavefronts per workgroup; W = look-back window; FZ: the small-grid
+// normaliser; THR: at most two rows' stores in flight per wavefront.
 //
 // Items are numbered chunk-major (item = chunk * nstream + j, j rotated to
 // the stream by the chunk index; see rotated_stream), so the chunk an item
 // waits on always has a smaller item number.
-template <typename TI, typename TO, int LPR, int R, int NW, int W, bool FZ>
+template <typename TI, typename TO, int LPR, int R, int NW, int W, bool FZ, bool THR>
 struct ChunkScan {
   static constexpr int VW = 16 / (int)sizeof(TI);  // channels per lane
   static constexpr int DG = LPR * VW;  // channels of one stream
@@ -728,6 +737,12 @@ struct ChunkScan {
           y[j] = st[j] * rz;
         }
         store_vec<TO, VW>(op + (int64_t)i * a.on, y);
+        // Throttled: the stores of a chunk's first rows queue in the CU's
+        // memory path ahead of the look-back polls and row loads of the
+        // other workgroups on the CU, which then wait behind them.
+        if constexpr (THR) {
+          if (i >= 2) wait_vmcnt<2 * (VW * (int)sizeof(TO) / 16)>();
+        }
         if (i == ifin) {
 #pragma unroll
           for (int j = 0; j < VW; ++j) a.fin[c0 + ds * VW + j] = st[j];
@@ -763,10 +778,10 @@ __device__ __forceinline__ unsigned read_epoch(const ScanArgs& a) {
 // items with smaller indices, which are dispatched first (workgroups are
 // dispatched in index order on each XCD), so the smallest unfinished item
 // can always run: no co-residency requirement and no ticket counter.
-template <typename TI, typename TO, int LPR, int R, int NW, int W, int WPE, bool FZ>
+template <typename TI, typename TO, int LPR, int R, int NW, int W, int WPE, bool FZ, bool THR>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, 8)))
 void scan_chunked(ScanArgs a) {
-  using CS = ChunkScan<TI, TO, LPR, R, NW, W, FZ>;
+  using CS = ChunkScan<TI, TO, LPR, R, NW, W, FZ, THR>;
   __shared__ typename CS::Smem sm;
   const unsigned epoch = read_epoch(a);
   const Pos p = pos_of(a, (int)blockIdx.x);
@@ -1574,13 +1589,18 @@ int launch_chunked(const ScanArgs& a, int64_t grid, hipStream_t s) {
     // 19.44 / 15.75 us; B=1 N=16384 H=12 (64) 17.45 / 13.81 / 12.49 us; B=1
     // N=8192 H=6 (32) 11.33 / 9.40 / 8.65 us; B=2 N=4096 H=12 (16) 8.99 /
     // 8.23 / -; B=8 N=1024 H=6 (4 chunks per stream) 7.00 / 6.89 / -.
-    auto* const k = a.nchunk > 16 ? scan_chunked<TI, TO, LPR, R, NW, 16, WPE, FZ>
-                  : a.nchunk > 4 ? scan_chunked<TI, TO, LPR, R, NW, 8, WPE, FZ>
-                                 : scan_chunked<TI, TO, LPR, R, NW, kW, WPE, FZ>;
+    auto* const k = a.nchunk > 16 ? scan_chunked<TI, TO, LPR, R, NW, 16, WPE, FZ, false>
+                  : a.nchunk > 4 ? scan_chunked<TI, TO, LPR, R, NW, 8, WPE, FZ, false>
+                                 : scan_chunked<TI, TO, LPR, R, NW, kW, WPE, FZ, false>;
     hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(NW * 64), 0, s, a);
   } else {
-    auto* const one_round = scan_chunked<TI, TO, LPR, R, NW, kW, WPE, FZ>;
-    auto* const rounds = scan_chunked<TI, TO, LPR, R, NW, kWRounds, WPE, FZ>;
+    // The resident grid throttles its stores (three workgroups per CU share
+    // the CU's memory path; THR): B=8 N=4096 H=12 D=64 bf16 18.13 -> 17.70
+    // us, same-box A/B, identical outputs.  Several rounds, and the small
+    // grids above, measured no gain (B=1 N=65536 H=16 D=128 +0.3%, B=2
+    // N=4096 H=12 +1%).
+    auto* const one_round = scan_chunked<TI, TO, LPR, R, NW, kW, WPE, FZ, true>;
+    auto* const rounds = scan_chunked<TI, TO, LPR, R, NW, kWRounds, WPE, FZ, false>;
     static const int per_cu = workgroups_per_cu(reinterpret_cast<const void*>(one_round), NW * 64);
     const int64_t resident = (int64_t)per_cu * cu_count();
     if (resident > 0 && grid > resident)
