@@ -105,8 +105,9 @@ def rotated_sets(torch, dev, shape, count: int, seed: int = 1):
     return sets
 
 
-def time_region(torch, launch, steps: int, warmup: int):
-    """(region ms over `steps` launches, per-launch event durations in ms)."""
+def time_region(torch, launch, steps: int, warmup: int, events: bool = True):
+    """(region ms over `steps` launches, per-launch event durations in ms, or
+    an empty list without `events`)."""
     for k in range(warmup):
         launch(k)
     torch.cuda.synchronize()
@@ -117,6 +118,8 @@ def time_region(torch, launch, steps: int, warmup: int):
     t1.record()
     torch.cuda.synchronize()
     region = t0.elapsed_time(t1)
+    if not events:
+        return region, []
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     for k in range(steps):
         evs[k][0].record()
@@ -530,7 +533,9 @@ def main() -> int:
     lam = c2_lam(H, torch).to(dev)
     launch = ScanLauncher(torch, kilat_amd, lam, sets, _lib.KDECAY_BF16)
     log(f"timing {args.steps} steps after {args.warmup} warm-up")
-    region, per = time_region(torch, launch, args.steps, args.warmup)
+    # No per-launch events here: they would add launches with gaps to the
+    # kernel trace that profiles/ summarises.
+    region, _ = time_region(torch, launch, args.steps, args.warmup, events=False)
     if launch.rc:
         raise RuntimeError("kdecay_scan_fwd failed: " + _lib.load().kdecay_last_error_string().decode())
     if kilat_amd.workspace_error(sets[0][0]):
@@ -543,8 +548,7 @@ def main() -> int:
     # launch stream over back-to-back launches, divided by the launch count
     # (events around every single launch would add their own gaps).
     achieved = value
-    log(f"region {ms_step * 1e3:.2f} us/step; events around single launches: mean {statistics.mean(per) * 1e3:.2f} us "
-        f"median {statistics.median(per) * 1e3:.2f} us")
+    log(f"region {ms_step * 1e3:.2f} us/step")
 
     result = {
         "metric": METRIC,
