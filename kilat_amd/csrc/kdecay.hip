@@ -555,7 +555,7 @@ struct ChunkScan {
   static_assert(G + 1 <= NT, "power table is filled one entry per thread");
 
   struct Smem {
-    float rz[L];      // 1 / z of each row of the chunk
+    alignas(16) float rz[L];  // 1 / z of each row of the chunk
     float pw[G + 1];  // lam^(R*k), k = 0..G
     float wt[NW][DG];  // per-wavefront totals (zero carry in)
     float carry[DG];   // F(chunk - 1)
@@ -728,11 +728,23 @@ struct ChunkScan {
     // stores of a chunk's first rows would otherwise queue in the CU's memory
     // path ahead of the look-back polls and row loads of the other
     // workgroups on the CU, which then wait behind them.
+    // The lane's normalisers, read at once (one LDS read per row left each
+    // row waiting on its own read: 0.5-1.4% on every shape measured).
+    static_assert(R % 4 == 0, "normalisers are read four at a time");
+    float rzl[R];
+#pragma unroll
+    for (int k = 0; k < R / 4; ++k) {
+      const float4 q = *reinterpret_cast<const float4*>(&sm.rz[g * R + 4 * k]);
+      rzl[4 * k] = q.x;
+      rzl[4 * k + 1] = q.y;
+      rzl[4 * k + 2] = q.z;
+      rzl[4 * k + 3] = q.w;
+    }
     auto row = [&](int i) {
       float v[VW], y[VW];
       opaque(raw[i]);
       unpack16<TI>(raw[i], v);
-      const float rz = sm.rz[g * R + i];
+      const float rz = rzl[i];
 #pragma unroll
       for (int j = 0; j < VW; ++j) {
         st[j] = __builtin_fmaf(lam, st[j], v[j]);
