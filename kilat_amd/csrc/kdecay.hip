@@ -1635,9 +1635,17 @@ int launch_chunked(const ScanArgs& a, int64_t grid, hipStream_t s) {
     // 19.44 / 15.75 us; B=1 N=16384 H=12 (64) 17.45 / 13.81 / 12.49 us; B=1
     // N=8192 H=6 (32) 11.33 / 9.40 / 8.65 us; B=2 N=4096 H=12 (16) 8.99 /
     // 8.23 / -; B=8 N=1024 H=6 (4 chunks per stream) 7.00 / 6.89 / -.
-    auto* const k = a.nchunk > 16 ? scan_chunked<TI, TO, LPR, R, NW, 16, WPE, FZ, false>
-                  : a.nchunk > 4 ? scan_chunked<TI, TO, LPR, R, NW, 8, WPE, FZ, false>
-                                 : scan_chunked<TI, TO, LPR, R, NW, kW, WPE, FZ, false>;
+    // Stores throttled (THR) when more than two workgroups share a CU on
+    // average: B=8 N=2048 H=12 D=64 (768 workgroups) 10.68 -> 10.52 us, B=4
+    // N=4096 H=12 11.10 -> 10.80 us; at 1.5 per CU (B=8 N=2048 H=6) it was
+    // 0.5% slower, and no change at fewer.
+    const bool thr = grid > 2 * (int64_t)cu_count();
+    auto* const k = a.nchunk > 16 ? (thr ? scan_chunked<TI, TO, LPR, R, NW, 16, WPE, FZ, true>
+                                         : scan_chunked<TI, TO, LPR, R, NW, 16, WPE, FZ, false>)
+                  : a.nchunk > 4  ? (thr ? scan_chunked<TI, TO, LPR, R, NW, 8, WPE, FZ, true>
+                                         : scan_chunked<TI, TO, LPR, R, NW, 8, WPE, FZ, false>)
+                                  : (thr ? scan_chunked<TI, TO, LPR, R, NW, kW, WPE, FZ, true>
+                                         : scan_chunked<TI, TO, LPR, R, NW, kW, WPE, FZ, false>);
     hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(NW * 64), 0, s, a);
   } else {
     // The resident grid throttles its stores (three workgroups per CU share

@@ -548,3 +548,20 @@ def test_small_grid_windows(hip_device, kdecay_lib, dname, H, N):
     assert_parity(y.cpu(), torch.from_numpy(ref).to(dtype), dtype, f"{dname} H={H} N={N}")
     assert rel_err(fin.cpu(), torch.from_numpy(sref)) <= 1e-5
     assert kilat_amd.workspace_error(V.to(hip_device)) == 0
+
+
+@pytest.mark.parametrize("dname,out,B,H,N", [("bf16", None, 8, 12, 2048), ("f32", None, 8, 12, 1024),
+                                             ("bf16", torch.float32, 8, 12, 2048), ("f16", None, 4, 12, 4096)])
+def test_small_grid_throttled_stores(hip_device, kdecay_lib, dname, out, B, H, N):
+    """Small-grid launches (256-row chunks) with more than two workgroups per
+    CU throttle their stores (768 workgroups here): one and two 16-byte stores
+    per row, a ragged last chunk, against the oracle, with the final state."""
+    dtype = DTYPES[dname]
+    g = torch.Generator().manual_seed(290 + N)
+    lam = lam_uniform(H, 0.5, 0.9999, g)
+    for n in (N, N - 37):
+        V = torch.randn(B, H, n, 64, generator=g).to(dtype)
+        y, fin = gpu_scan(lam, V, hip_device, return_final_state=True, out_dtype=out)
+        ref, sref = O.scan(lam, V, out_dtype=out)
+        assert_parity(y, ref, out or dtype, f"{dname} N={n}")
+        assert rel_err(fin, sref) <= 1e-5
