@@ -1650,9 +1650,8 @@ int launch_chunked(const ScanArgs& a, int64_t grid, hipStream_t s) {
   } else {
     // The resident grid throttles its stores (three workgroups per CU share
     // the CU's memory path; THR): B=8 N=4096 H=12 D=64 bf16 18.13 -> 17.70
-    // us, same-box A/B, identical outputs.  Several rounds, and the small
-    // grids above, measured no gain (B=1 N=65536 H=16 D=128 +0.3%, B=2
-    // N=4096 H=12 +1%).
+    // us, same-box A/B, identical outputs.  Launches in several rounds
+    // measured no gain (B=1 N=65536 H=16 D=128 +0.3%).
     auto* const one_round = scan_chunked<TI, TO, LPR, R, NW, kW, WPE, FZ, true>;
     auto* const rounds = scan_chunked<TI, TO, LPR, R, NW, kWRounds, WPE, FZ, false>;
     static const int per_cu = workgroups_per_cu(reinterpret_cast<const void*>(one_round), NW * 64);
