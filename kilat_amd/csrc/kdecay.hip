@@ -1505,8 +1505,11 @@ __global__ __launch_bounds__(256) void copy_state(const float* init, float* fin,
 // --------------------------------------------------------------------------
 thread_local char g_err[512] = "";
 
-// Poll limit of the bounded waits of the next launches (kdecay_debug_set_spin_limit).
+// Poll limit of the bounded waits of the next launches (kdecay_debug_set_spin_limit);
+// read and written atomically, since host threads may launch concurrently.
 static int g_spin_limit = kSpinLimit;
+
+int spin_limit() { return __atomic_load_n(&g_spin_limit, __ATOMIC_RELAXED); }
 
 int fail(int code, const char* fmt, ...) {
   va_list ap;
@@ -1856,8 +1859,8 @@ const char* kdecay_version(void) { return "kdecay 0.1.0 gfx950"; }
 const char* kdecay_last_error_string(void) { return g_err; }
 
 int kdecay_debug_set_spin_limit(int polls) {
-  const int previous = g_spin_limit;
-  g_spin_limit = polls > 0 && polls < kSpinLimit ? polls : kSpinLimit;
+  const int previous =
+      __atomic_exchange_n(&g_spin_limit, polls > 0 && polls < kSpinLimit ? polls : kSpinLimit, __ATOMIC_RELAXED);
   return previous == kSpinLimit ? 0 : previous;
 }
 
@@ -1934,7 +1937,7 @@ static int scan_fwd_impl(const void* V, int v_dtype, const int64_t* v_strides, v
   a.f_ng = make_fastdiv((uint32_t)a.ng);
   a.f_H = make_fastdiv((uint32_t)H);
   a.hdr = need ? static_cast<unsigned*>(workspace) : nullptr;
-  a.spin_limit = g_spin_limit;
+  a.spin_limit = spin_limit();
   a.flags = need ? reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes) : nullptr;
   a.state_rows = bwd_chunk_rows(B, H, N, D, v_dtype);
   a.nsaved = (N + a.state_rows - 1) / a.state_rows;
@@ -2091,7 +2094,7 @@ int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides, const 
   a.f_H = make_fastdiv((uint32_t)H);
   a.f_nchunk = make_fastdiv((uint32_t)nchunk);
   a.hdr = static_cast<unsigned*>(workspace);
-  a.spin_limit = g_spin_limit;
+  a.spin_limit = spin_limit();
   const size_t flag_bytes = nchunk > 1 ? (size_t)(B * H * nchunk * D) * sizeof(u64) : 0;
   a.flags = nchunk > 1 ? reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes) : nullptr;
   a.partial = reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes + flag_bytes);
