@@ -318,8 +318,8 @@ def bench_backward(torch, dev, steps=100):
                                      None, states.data_ptr(), None, dlam.data_ptr(), None, B, H, N, D, 0,
                                      ws.data_ptr(), ws.numel(), stream)
 
-    rf, _ = time_region(torch, fwd, steps, 10)
-    rb, _ = time_region(torch, bwd, steps, 10)
+    rf, _ = time_region(torch, fwd, steps, 100, events=False)
+    rb, _ = time_region(torch, bwd, steps, 100, events=False)
     if rc[0]:
         raise RuntimeError("training scan failed: " + lib.kdecay_last_error_string().decode())
     n = B * H * N * D
