@@ -176,13 +176,24 @@ __device__ __forceinline__ float z_of(float lam, int64_t t) {
 // The same values with lower latency, for the decode step, where z is on the
 // critical path of a launch-latency-bound kernel: for e < 2^16 the binary
 // exponentiation is unrolled and branch-free (the same products in the same
-// order as ipow_f64; squarings past the top bit do not reach r), and the
-// small cases are selects instead of branches.  The scan kernels keep the
+// order as ipow_f64; squarings past the top bit do not reach r), 12 steps
+// instead of 16 for e < 2^12 (C3 decode step 2.22 -> 2.18 us), and the small
+// cases are selects instead of branches.  The scan kernels keep the
 // loop: they build their z tables while their rows are in flight, and there
 // the shorter form measured 3.7% slower (bf16, B=8 N=4096 H=12 D=64).
 __device__ __forceinline__ float pow_like_torch_fast(float x, int64_t e) {
   double r;
-  if (e >= 0 && e < (1 << 16)) {
+  if (e >= 0 && e < (1 << 12)) {
+    const unsigned u = (unsigned)e;
+    double xd = (double)x;
+    r = 1.0;
+#pragma unroll
+    for (int k = 0; k < 12; ++k) {
+      const double rx = r * xd;
+      r = (u >> k) & 1u ? rx : r;
+      xd *= xd;
+    }
+  } else if (e >= 0 && e < (1 << 16)) {
     const unsigned u = (unsigned)e;
     double xd = (double)x;
     r = 1.0;
