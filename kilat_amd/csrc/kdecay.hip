@@ -1668,20 +1668,21 @@ int launch_chunked(const ScanArgs& a, int64_t grid, hipStream_t s) {
     // measured no gain (B=1 N=65536 H=16 D=128 +0.3%).
     auto* const one_round = scan_chunked<TI, TO, LPR, R, NW, kW, WPE, FZ, true>;
     auto* const rounds = scan_chunked<TI, TO, LPR, R, NW, kWRounds, WPE, FZ, false>;
-    // Several rounds with at most 12 resident chunk rows per stream: a window
-    // of 1 (each chunk waits for its predecessor's inclusive word, mostly
-    // already published in an earlier round).  Measured (bf16, same-box A/B,
-    // window 1 against 2): B=8 N=8192 H=12 D=64 (8 rows per round) 35.1 /
-    // 39.3 us, B=5 N=16384 H=16 D=64 (9.6) 56.3 / 60.9, B=2 N=65536 H=16
-    // D=128 (12) 179.1 / 187.1, B=4 N=16384 H=16 D=128 (6) 96.1 / 98.3; with
-    // more rows per round window 2 wins: B=7 N=16384 H=8 D=64 (13.7) 43.4 /
-    // 42.1, B=4 N=16384 H=12 D=64 (16) 39.6 / 35.3, B=1 N=65536 H=16 D=128
-    // (24) 106 / 91.5.
+    // Several rounds with at most 16 resident chunk rows per stream (resident
+    // workgroups over streams): a window of 1 (each chunk waits for its
+    // predecessor's inclusive word, mostly already published in an earlier
+    // round).  Measured (bf16, 4 workgroups per CU, same-box A/B, window 1
+    // against 2): B=8 N=8192 H=12 D=64 (10.7 rows per round) 35.1 / 39.3 us,
+    // B=5 N=16384 H=16 D=64 (12.8) 56.3 / 60.9, B=2 N=65536 H=16 D=128 (16)
+    // 179.1 / 187.1, B=4 N=16384 H=16 D=128 (8) 96.1 / 98.3; with more rows
+    // per round window 2 wins: B=7 N=16384 H=8 D=64 (18.3) 43.4 / 42.1, B=4
+    // N=16384 H=12 D=64 (21.3) 39.6 / 35.3, B=1 N=65536 H=16 D=128 (32) 106 /
+    // 91.5.
     auto* const rounds1 = scan_chunked<TI, TO, LPR, R, NW, 1, WPE, FZ, false>;
     static const int per_cu = workgroups_per_cu(reinterpret_cast<const void*>(one_round), NW * 64);
     const int64_t resident = (int64_t)per_cu * cu_count();
     if (resident > 0 && grid > resident)
-      hipLaunchKernelGGL(resident <= 12 * (int64_t)a.nstream ? rounds1 : rounds, dim3((unsigned)grid), dim3(NW * 64), 0,
+      hipLaunchKernelGGL(resident <= 16 * (int64_t)a.nstream ? rounds1 : rounds, dim3((unsigned)grid), dim3(NW * 64), 0,
                          s, a);
     else
       hipLaunchKernelGGL(one_round, dim3((unsigned)grid), dim3(NW * 64), 0, s, a);

@@ -96,7 +96,7 @@ def test_scan_shapes_large_grid(hip_device, kdecay_lib, dname, D):
 @pytest.mark.parametrize("dname,out", [("f32", None), ("f16", None), ("bf16", torch.float32)])
 def test_scan_several_rounds(hip_device, kdecay_lib, dname, out):
     """1152 chunks of 512 rows: more than the device holds at once, so the
-    launch runs in rounds; with 128 streams at most 12 chunk rows per stream
+    launch runs in rounds; with 128 streams at most 16 chunk rows per stream
     are resident, so it takes the window-1 kernels of each type (the C4 tests
     take the window-2 ones)."""
     dtype = DTYPES[dname]
