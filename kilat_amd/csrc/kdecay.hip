@@ -1607,13 +1607,14 @@ int64_t chunk_rows(int v_dtype, int64_t D, ChunkShape c) {
 
 // Chunk shape of a problem: (kR, kNW), or (kRSmall, kNWSmall) when a
 // (kR, kNW) grid would have at most kSmallGrid chunks and leave most of the
-// device idle.  Measured on MI355X (bf16, D=64/128): 8 rows per lane were
-// 10-18% faster for grids of 96-384 chunks at 16 rows, and 6-7% slower for
-// grids of 768-1024.  The rule uses the shape only, so
+// device idle.  Measured on MI355X (bf16, D=64, same-box A/B of the current
+// kernels, 16 rows against 8): 360 chunks at 16 rows 11.46 / 10.11 us, 384
+// 11.43 / 10.67, 416 11.60 / 11.62, 448 11.86 / 11.99, 480 12.04 / 12.65,
+// 512 12.43 / 13.05, 576 14.52 / 14.94.  The rule uses the shape only, so
 // kdecay_scan_workspace_bytes can apply it too.
 constexpr int kRSmall = 8;
 constexpr int kNWSmall = 4;
-constexpr int64_t kSmallGrid = 512;
+constexpr int64_t kSmallGrid = 416;
 
 ChunkShape chunk_shape(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   const int64_t L = chunk_rows(v_dtype, D, ChunkShape{kR, kNW});

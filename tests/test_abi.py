@@ -52,7 +52,7 @@ def test_workspace_bytes(kdecay_lib):
     ws = kdecay_lib.kdecay_scan_workspace_bytes
     # A stream is a (b,h) pair and a 128-byte channel group; a chunk holds 64 KiB of
     # input: 512 rows of a 128-byte group, or half that (8 rows per lane instead of
-    # 16) when the 16-row grid has at most 512 chunks.  Words: one per channel per chunk.
+    # 16) when the 16-row grid has at most 416 chunks.  Words: one per channel per chunk.
     assert ws(8, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + 8 * 12 * 8 * 64 * 8  # 768 chunks
     assert ws(1, 16, 65536, 128, _lib.KDECAY_BF16) == 256 + 16 * 128 * 128 * 8  # 4096 chunks
     assert ws(2, 6, 512, 64, _lib.KDECAY_BF16) == 256 + 2 * 6 * 2 * 64 * 8  # small grid: 256-row chunks
@@ -60,13 +60,15 @@ def test_workspace_bytes(kdecay_lib):
     assert ws(2, 6, 1024, 64, _lib.KDECAY_F32) == 256 + 2 * 6 * 4 * 64 * 8  # 2 groups of 32, 256-row chunks
     assert ws(1, 2, 4096, 32, _lib.KDECAY_BF16) == 256 + 2 * 8 * 32 * 8  # 32-channel rows: 512-row chunks
     assert ws(8, 12, 2048, 64, _lib.KDECAY_BF16) == 256 + 8 * 12 * 8 * 64 * 8  # 384 chunks at 16 rows: 8
+    assert ws(4, 13, 4096, 64, _lib.KDECAY_BF16) == 256 + 4 * 13 * 16 * 64 * 8  # 416 chunks at 16 rows: 8
+    assert ws(4, 13, 4097, 64, _lib.KDECAY_BF16) == 256 + 4 * 13 * 9 * 64 * 8  # 468: 16 rows
     assert ws(2, 6, 1024, 48, _lib.KDECAY_BF16) == 0  # unsupported D
 
 
 def test_backward_workspace_bytes(kdecay_lib):
     wb = kdecay_lib.kdecay_scan_bwd_workspace_bytes
     # 512-row chunks (16 rows x 4 wavefronts x 8 row groups for a 128-byte
-    # group), or 128-row chunks (4 rows) when the 512-row grid has at most 512
+    # group), or 128-row chunks (4 rows) when the 512-row grid has at most 256
     # chunks; header + look-back words (one per channel per chunk) + one
     # 8-byte tagged dlam partial per chunk of every stream, rounded up to 256
     # bytes.

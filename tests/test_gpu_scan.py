@@ -26,7 +26,7 @@ DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
 def chunk_rows(dtype, D, rows_per_lane=16):
     """Rows per chunk of the library's scan: 256 lanes x 16 rows x 16 bytes of one
     channel group of at most 128 bytes (8 rows per lane when the 16-row grid has
-    at most 512 chunks)."""
+    at most 416 chunks)."""
     es = torch.empty((), dtype=dtype).element_size()
     dg = min(D, 128 // es)
     return 4 * (64 // (dg // (16 // es))) * rows_per_lane
@@ -75,7 +75,7 @@ def test_scan_shapes(hip_device, kdecay_lib, dname, D):
 @pytest.mark.parametrize("dname", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
 def test_scan_shapes_large_grid(hip_device, kdecay_lib, dname, D):
-    """Grids of more than 512 chunks at 16 rows per lane: the 16-row kernels,
+    """Grids of more than 416 chunks at 16 rows per lane: the 16-row kernels,
     with a ragged last chunk and a chunk boundary at the end."""
     dtype = DTYPES[dname]
     es = torch.empty((), dtype=dtype).element_size()
@@ -171,13 +171,13 @@ def test_mixed_shapes_share_one_workspace(hip_device, kdecay_lib):
 
 @pytest.mark.parametrize("N", [4096, 4097])
 def test_chunk_size_switch(hip_device, kdecay_lib, N):
-    """64 streams of bf16 D=64: N=4096 is exactly 512 chunks of 512 rows (the
-    library takes 256-row chunks), N=4097 is 576 (it keeps 512-row chunks)."""
+    """52 streams of bf16 D=64: N=4096 is exactly 416 chunks of 512 rows (the
+    library takes 256-row chunks), N=4097 is 468 (it keeps 512-row chunks)."""
     g = torch.Generator().manual_seed(170)
-    lam = lam_uniform(8, 0.5, 0.9999, g)
-    V = torch.randn(8, 8, N, 64, generator=g).to(torch.bfloat16)
-    ws = kdecay_lib.kdecay_scan_workspace_bytes(8, 8, N, 64, 1)
-    assert ws == 256 + 8 * 8 * (16 if N == 4096 else 9) * 64 * 8
+    lam = lam_uniform(13, 0.5, 0.9999, g)
+    V = torch.randn(4, 13, N, 64, generator=g).to(torch.bfloat16)
+    ws = kdecay_lib.kdecay_scan_workspace_bytes(4, 13, N, 64, 1)
+    assert ws == 256 + 4 * 13 * (16 if N == 4096 else 9) * 64 * 8
     y, fin = gpu_scan(lam, V, hip_device, return_final_state=True)
     ref, sref = O.scan(lam, V)
     assert_parity(y, ref, torch.bfloat16, f"N={N}")
@@ -312,7 +312,7 @@ def test_fp32_output_for_bf16_input(hip_device, kdecay_lib, B, H):
 @pytest.mark.parametrize("B,H", [(2, 3), (24, 8)])
 def test_chunked_prefill_with_carry(hip_device, kdecay_lib, dname, B, H):
     """Split prefill with a carried state and a position offset, on small grids
-    and on grids of more than 512 chunks (the two chunk sizes)."""
+    and on grids of more than 416 chunks (the two chunk sizes)."""
     dtype = DTYPES[dname]
     lam, V = c1_inputs(B=B, N=1500, H=H, D=64)
     V = V.to(dtype)
@@ -535,7 +535,7 @@ def test_scan_wide_and_padded_head_dims(hip_device, kdecay_lib, dname, D):
 @pytest.mark.parametrize("dname,H,N", [("bf16", 3, 2000), ("bf16", 2, 5000), ("bf16", 1, 40000), ("f32", 2, 9000),
                                        ("f16", 1, 70000)])
 def test_small_grid_windows(hip_device, kdecay_lib, dname, H, N):
-    """Small grids (at most 512 chunks of 512 rows) of few streams with long
+    """Small grids (at most 416 chunks of 512 rows) of few streams with long
     chains: the one-round launch takes a look-back window of 4, 8 or 16 by
     chunks per stream (8 rows per lane: 256-row chunks for 128-byte groups).
     Against the C restatement at full length, with a carried state and an
