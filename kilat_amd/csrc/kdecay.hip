@@ -1719,18 +1719,27 @@ constexpr int kRB = 16;
 constexpr int kRBSmall = 4;
 constexpr int kNWB = 4;
 constexpr int64_t kBwdSmallGrid = 256;
+constexpr int64_t kBwdShortChainGrid = 384;
 
 // 4 rows per lane when the 16-row grid has at most kBwdSmallGrid chunks, so
-// that the 4-row grid (4x the workgroups) still runs in one round; its long
-// chains would otherwise run in several rounds with a narrow window.
-// Measured (bf16 D=64, same-box A/B): B=8 N=1024 H=6 (96 chunks at 16 rows)
-// 4 rows 11.7 us, 16 rows 17.4 us; B=1 N=32768 H=6 (384) 4 rows 84 us.
+// that the 4-row grid (4x the workgroups) still runs in one round, or at most
+// kBwdShortChainGrid chunks with chains of at most 4 (the 4-row grid then
+// takes 1.5 rounds of chains at most 16 chunks long); longer chains in
+// several rounds run with a narrow window and lose.  Measured (same-box A/B,
+// bf16, 4 rows vs 16 rows, us): D=64 B=8 N=1024 H=6 (96 chunks at 16 rows)
+// 11.3 / 16.2; B=8 N=2048 H=10 (320, 4 per stream) 19.1 / 21.1; B=8 N=2048
+// H=12 (384, 4) 20.1 / 21.8; B=12 N=1024 H=16 (384, 2) 20.5 / 22.6; B=4
+// N=4096 H=12 (384, 8) 22.9 / 22.2; B=2 N=8192 H=12 (384, 16) 31.7 / 22.3;
+// B=8 N=2048 H=14 (448, 4) 23.2 / 22.9; D=32 B=8 N=4096 H=12 (384, 4)
+// 24.5 / 28.6; D=32 B=8 N=4096 H=16 (512, 4) 32.4 / 29.8.
 int bwd_rows_per_lane(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   const int64_t vw = 16 / elem_size(v_dtype);
   const int64_t DG = group_width(v_dtype, D);
   const int64_t L = kNWB * (64 / (DG / vw)) * kRB;
   const int64_t nstream = B * H * (D / DG);
-  return (N + L - 1) / L * nstream <= kBwdSmallGrid ? kRBSmall : kRB;
+  const int64_t chain = (N + L - 1) / L;
+  const int64_t grid = chain * nstream;
+  return grid <= kBwdSmallGrid || (grid <= kBwdShortChainGrid && chain <= 4) ? kRBSmall : kRB;
 }
 
 int64_t bwd_chunk_rows(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {

@@ -69,13 +69,21 @@ def test_backward_workspace_bytes(kdecay_lib):
     wb = kdecay_lib.kdecay_scan_bwd_workspace_bytes
     # 512-row chunks (16 rows x 4 wavefronts x 8 row groups for a 128-byte
     # group), or 128-row chunks (4 rows) when the 512-row grid has at most 256
-    # chunks; header + look-back words (one per channel per chunk) + one
+    # chunks, or at most 384 with at most 4 per stream; header + look-back words (one per channel per chunk) + one
     # 8-byte tagged dlam partial per chunk of every stream, rounded up to 256
     # bytes.
     nst, nch = 8 * 12, 4096 // 512
     assert wb(8, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
     nst, nch = 8 * 6, 1024 // 128  # 96 chunks at 512 rows: the small-grid shape
     assert wb(8, 6, 1024, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    nst, nch = 8 * 12, 2048 // 128  # 384 chunks at 512 rows, 4 per stream
+    assert wb(8, 12, 2048, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    nst, nch = 8 * 12, 5  # 480 chunks at 512 rows, 5 per stream: 512-row chunks
+    assert wb(8, 12, 2049, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    nst, nch = 4 * 12, 4096 // 512  # 384 chunks, 8 per stream: 512-row chunks
+    assert wb(4, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    nst, nch = 8 * 14, 2048 // 512  # 448 chunks, 4 per stream: 512-row chunks
+    assert wb(8, 14, 2048, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
     # one chunk per stream: no look-back words, but the header and the partials
     assert wb(2, 6, 100, 64, _lib.KDECAY_BF16) == 256 + 256
     assert wb(2, 6, 100, 48, _lib.KDECAY_BF16) == 0  # unsupported D

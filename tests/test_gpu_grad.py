@@ -200,6 +200,27 @@ def test_backward_init_final_offset_large_grid(hip_device, kdecay_lib, dname):
     check(dv, dl, di, rdv, rdl, rdi, dtype, f"large grid {dname}")
 
 
+@pytest.mark.parametrize("dname,B,H,N,D", [("bf16", 8, 12, 2048, 64), ("bf16", 8, 12, 2049, 64),
+                                             ("f16", 8, 14, 2048, 64), ("f32", 4, 12, 2048, 64),
+                                             ("bf16", 8, 12, 4096, 32)])
+def test_backward_short_chain_grids(hip_device, kdecay_lib, dname, B, H, N, D):
+    """Grids of 320-448 chunks at 512 rows (1024 for D=32): with chains of at
+    most 4 chunks up to 384 of them the backward takes 128-row chunks (1536
+    workgroups, more than one round), otherwise 512-row ones (N=2049: chains
+    of 5; H=14: 448 chunks).  Carry-in state, final-state gradient and a
+    position offset, against the fp64 adjoint recurrence."""
+    dtype = DTYPES[dname]
+    g = torch.Generator().manual_seed(216 + H + N % 7)
+    lam = lam_uniform(H, 0.7, 0.9999, g)
+    V = torch.randn(B, H, N, D, generator=g).to(dtype)
+    gy = torch.randn(B, H, N, D, generator=g).to(dtype)
+    init = torch.randn(B, H, D, generator=g)
+    gfin = torch.randn(B, H, D, generator=g)
+    dv, dl, di = gpu_grads(lam, V, gy, hip_device, init=init, gfin=gfin, t_offset=5)
+    rdv, rdl, rdi = O.scan_grads_f64(lam, V, gy, init_state=init, gfin=gfin, t_offset=5)
+    check(dv, dl, di, rdv, rdl, rdi, dtype, f"{dname} {B}x{H}x{N}x{D}")
+
+
 def test_backward_c1_shape_and_drop_in(hip_device, kdecay_lib):
     """C1 (B=2 N=1024 H=6 D=64 fp32) through triton_global_decay, as a training step calls it."""
     g = torch.Generator().manual_seed(211)
