@@ -1606,20 +1606,33 @@ int64_t chunk_rows(int v_dtype, int64_t D, ChunkShape c) {
 }
 
 // Chunk shape of a problem: (kR, kNW), or (kRSmall, kNWSmall) when a
-// (kR, kNW) grid would have at most kSmallGrid chunks and leave most of the
-// device idle.  Measured on MI355X (bf16, D=64, same-box A/B of the current
-// kernels, 16 rows against 8): 360 chunks at 16 rows 11.46 / 10.11 us, 384
-// 11.43 / 10.67, 416 11.60 / 11.62, 448 11.86 / 11.99, 480 12.04 / 12.65,
-// 512 12.43 / 13.05, 576 14.52 / 14.94.  The rule uses the shape only, so
+// (kR, kNW) grid would leave most of the device idle: at most kSmallGrid
+// chunks, kSmallGrid2 with 2 chunks per stream (the 8-row grid, 2x the
+// workgroups, still resident at five per CU) and kSmallGrid1 with 1 (the
+// 16-row grid then needs no look-back at all, the 8-row one a chain of 2).
+// Measured on MI355X (bf16, same-box A/B of the current kernels, 16 rows
+// against 8, us; chunks at 16 rows): D=64 N=2048 B=8, 4 per stream: H=12
+// (384) 11.62 / 10.58, H=14 (448) 11.87 / 11.96, H=16 (512) 12.46 / 12.99;
+// N=1024 H=16, 2 per stream: B=16 (512) 13.56 /
+// 12.72, B=19 (608) 15.19 / 14.84, B=20 (640) 15.48 / 15.40, B=21 (672)
+// 15.64 / 18.69; D=128 N=1024 H=16 B=10 (640) 17.21 / 15.65, B=11 (704)
+// 17.32 / 19.56; N=512 H=16, 1 per stream: B=8 (128) 7.42 / 7.16, B=10
+// (160) 7.68 / 7.63, B=12 (192) 7.95 / 8.04, B=16 (256) 8.75 / 9.75, B=24
+// (384) 10.18 / 11.53.  Long chains keep the 8-row grid (B=1 N=65536 H=2,
+// 256 chunks: 26.42 / 20.41).  The rule uses the shape only, so
 // kdecay_scan_workspace_bytes can apply it too.
 constexpr int kRSmall = 8;
 constexpr int kNWSmall = 4;
 constexpr int64_t kSmallGrid = 416;
+constexpr int64_t kSmallGrid2 = 640;
+constexpr int64_t kSmallGrid1 = 160;
 
 ChunkShape chunk_shape(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   const int64_t L = chunk_rows(v_dtype, D, ChunkShape{kR, kNW});
   const int64_t nstream = B * H * (D / group_width(v_dtype, D));
-  if ((N + L - 1) / L * nstream <= kSmallGrid) return ChunkShape{kRSmall, kNWSmall};
+  const int64_t chain = (N + L - 1) / L;
+  const int64_t lim = chain == 1 ? kSmallGrid1 : chain == 2 ? kSmallGrid2 : kSmallGrid;
+  if (chain * nstream <= lim) return ChunkShape{kRSmall, kNWSmall};
   return ChunkShape{kR, kNW};
 }
 

@@ -52,7 +52,8 @@ def test_workspace_bytes(kdecay_lib):
     ws = kdecay_lib.kdecay_scan_workspace_bytes
     # A stream is a (b,h) pair and a 128-byte channel group; a chunk holds 64 KiB of
     # input: 512 rows of a 128-byte group, or half that (8 rows per lane instead of
-    # 16) when the 16-row grid has at most 416 chunks.  Words: one per channel per chunk.
+    # 16) when the 16-row grid has at most 416 chunks (640 with 2 chunks per stream,
+    # 160 with 1).  Words: one per channel per chunk.
     assert ws(8, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + 8 * 12 * 8 * 64 * 8  # 768 chunks
     assert ws(1, 16, 65536, 128, _lib.KDECAY_BF16) == 256 + 16 * 128 * 128 * 8  # 4096 chunks
     assert ws(2, 6, 512, 64, _lib.KDECAY_BF16) == 256 + 2 * 6 * 2 * 64 * 8  # small grid: 256-row chunks
@@ -62,6 +63,10 @@ def test_workspace_bytes(kdecay_lib):
     assert ws(8, 12, 2048, 64, _lib.KDECAY_BF16) == 256 + 8 * 12 * 8 * 64 * 8  # 384 chunks at 16 rows: 8
     assert ws(4, 13, 4096, 64, _lib.KDECAY_BF16) == 256 + 4 * 13 * 16 * 64 * 8  # 416 chunks at 16 rows: 8
     assert ws(4, 13, 4097, 64, _lib.KDECAY_BF16) == 256 + 4 * 13 * 9 * 64 * 8  # 468: 16 rows
+    assert ws(20, 16, 1024, 64, _lib.KDECAY_BF16) == 256 + 20 * 16 * 4 * 64 * 8  # 640, 2 per stream: 8 rows
+    assert ws(21, 16, 1024, 64, _lib.KDECAY_BF16) == 256 + 21 * 16 * 2 * 64 * 8  # 672: 16 rows
+    assert ws(10, 16, 512, 64, _lib.KDECAY_BF16) == 256 + 10 * 16 * 2 * 64 * 8  # 160, 1 per stream: 8 rows
+    assert ws(11, 16, 512, 64, _lib.KDECAY_BF16) == 0  # 176 single-chunk streams: 16 rows, no look-back
     assert ws(2, 6, 1024, 48, _lib.KDECAY_BF16) == 0  # unsupported D
 
 

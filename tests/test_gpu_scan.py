@@ -26,7 +26,7 @@ DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
 def chunk_rows(dtype, D, rows_per_lane=16):
     """Rows per chunk of the library's scan: 256 lanes x 16 rows x 16 bytes of one
     channel group of at most 128 bytes (8 rows per lane when the 16-row grid has
-    at most 416 chunks)."""
+    at most 416 chunks, 640 at 2 chunks per stream, 160 at 1)."""
     es = torch.empty((), dtype=dtype).element_size()
     dg = min(D, 128 // es)
     return 4 * (64 // (dg // (16 // es))) * rows_per_lane
@@ -75,14 +75,14 @@ def test_scan_shapes(hip_device, kdecay_lib, dname, D):
 @pytest.mark.parametrize("dname", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
 def test_scan_shapes_large_grid(hip_device, kdecay_lib, dname, D):
-    """Grids of more than 416 chunks at 16 rows per lane: the 16-row kernels,
-    with a ragged last chunk and a chunk boundary at the end."""
+    """Grids of more than 640 chunks at 16 rows per lane, 2 per stream: the
+    16-row kernels, with a ragged last chunk and a chunk boundary at the end."""
     dtype = DTYPES[dname]
     es = torch.empty((), dtype=dtype).element_size()
     ng = D // min(D, 128 // es)
     L = chunk_rows(dtype, D, 16)
     H = 8
-    B = -(-300 // (H * ng))  # at least 300 streams: 2 chunks each exceed 512
+    B = -(-336 // (H * ng))  # at least 336 streams: 2 chunks each exceed 640
     g = torch.Generator().manual_seed(150 + D)
     lam = lam_uniform(H, 0.5, 0.9999, g)
     for N in (L + 5, 2 * L):
@@ -181,6 +181,24 @@ def test_chunk_size_switch(hip_device, kdecay_lib, N):
     y, fin = gpu_scan(lam, V, hip_device, return_final_state=True)
     ref, sref = O.scan(lam, V)
     assert_parity(y, ref, torch.bfloat16, f"N={N}")
+    assert rel_err(fin, sref) <= 1e-5
+
+
+@pytest.mark.parametrize("B,N,nchunk", [(20, 1024, 4), (21, 1024, 2), (10, 512, 2), (11, 512, 0)])
+def test_chunk_size_switch_short_chains(hip_device, kdecay_lib, B, N, nchunk):
+    """16 heads of bf16 D=64 with 2 chunks of 512 rows per stream: 640 chunks
+    (B=20) take 256-row chunks, 672 (B=21) keep 512-row ones; with 1 chunk per
+    stream 160 (B=10) take 256-row chunks, 176 (B=11) run without look-back.
+    Against the C restatement with a carried state and an offset."""
+    g = torch.Generator().manual_seed(171 + B)
+    lam = lam_uniform(16, 0.5, 0.9999, g)
+    V = torch.randn(B, 16, N, 64, generator=g).to(torch.bfloat16)
+    init = torch.randn(B, 16, 64, generator=g)
+    ws = kdecay_lib.kdecay_scan_workspace_bytes(B, 16, N, 64, 1)
+    assert ws == (256 + B * 16 * nchunk * 64 * 8 if nchunk else 0)
+    y, fin = gpu_scan(lam, V, hip_device, initial_state=init.to(hip_device), return_final_state=True, t_offset=9)
+    ref, sref = O.scan(lam, V, init_state=init, t_offset=9)
+    assert_parity(y, ref, torch.bfloat16, f"B={B} N={N}")
     assert rel_err(fin, sref) <= 1e-5
 
 
