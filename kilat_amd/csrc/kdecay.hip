@@ -485,6 +485,16 @@ __device__ __forceinline__ uint4 load16_buffer(__amdgpu_buffer_rsrc_t r, unsigne
 // The launch epoch from the workspace header, kept in a vector register:
 // read through a uniform address, the value was moved to a scalar register
 // at once, which waited for the load (and every load issued before it).
+// One of n workgroups that each finish a launch's use of the epoch: the
+// last of them resets the count and advances the epoch for the next launch.
+__device__ __forceinline__ void count_done(unsigned* hdr, unsigned n, unsigned epoch) {
+  const unsigned d = __hip_atomic_fetch_add(hdr + HDR_DONE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (d == n - 1u) {
+    __hip_atomic_store(hdr + HDR_DONE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(hdr + HDR_EPOCH, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 __device__ __forceinline__ unsigned read_epoch_v(const unsigned* hdr) {
   unsigned zero;
   asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
@@ -696,14 +706,9 @@ struct ChunkScan {
     // every earlier chunk of the stream, each written after its workgroup
     // read the epoch.  When the last chunk of every stream is here, every
     // workgroup of this launch has read the epoch (each holds at least one
-    // item): advance it for the next launch.
-    if (multi && last && tid == 0) {
-      const unsigned d = __hip_atomic_fetch_add(a.hdr + HDR_DONE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (d == (unsigned)a.nstream - 1u) {
-        __hip_atomic_store(a.hdr + HDR_DONE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(a.hdr + HDR_EPOCH, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
+    // item): advance it for the next launch.  (Counted after the stores
+    // instead, C2 measured 1.7% slower and the small grids 2.5%.)
+    if (multi && last && tid == 0) count_done(a.hdr, (unsigned)a.nstream, epoch);
 
     // The lane's true start state.
     float ew[VW];  // state before this wavefront's first row, zero carry into the chunk
@@ -873,8 +878,14 @@ struct BwdArgs {
   u64* flags;
   unsigned* hdr;
   int spin_limit;  // as ScanArgs::spin_limit, for the look-back and the dlam reduction
+  int ndone;       // workgroups that count toward the epoch's advance (ChunkBwd::run)
+  int per_stream;  // 1: the first chunk of every stream counts instead
   FastDiv f_nstream, f_ng, f_H, f_nchunk;  // division by nstream, ng, H and nchunk
 };
+
+// XCDs of the device: workgroups are handed to them round-robin by index, and
+// each XCD dispatches its share in index order.
+constexpr int kXcds = 8;
 
 // d(1/z)/dlam for z = (1 - lam^e) / ((1 - lam) + 1e-6), evaluated in double.
 __device__ __forceinline__ float dinvz_dlam(float lam, int64_t e) {
@@ -1289,16 +1300,9 @@ struct ChunkBwd {
       }
     }
 
-    // Chunk 0 is the last of its stream in this order; see ChunkScan.  (With
-    // one chunk per stream every workgroup is a chunk 0: the epoch still
-    // advances, for the dlam partials' tags.)
-    if (chunk == 0 && tid == 0) {
-      const unsigned d = __hip_atomic_fetch_add(a.hdr + HDR_DONE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (d == (unsigned)a.nstream - 1u) {
-        __hip_atomic_store(a.hdr + HDR_DONE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(a.hdr + HDR_EPOCH, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
+    // Few streams: the first chunk of each stream counts, as soon as its
+    // look-back is done (see the end of run()).
+    if (a.per_stream && chunk == 0 && tid == 0) count_done(a.hdr, (unsigned)a.nstream, epoch);
 
     // dV with the true carry.
     float gn[VW];
@@ -1314,7 +1318,23 @@ struct ChunkBwd {
     // The workgroup with the largest item index of head h sums the head's
     // partials.  Every other item of the head has a smaller index, so it was
     // dispatched earlier and finishes without waiting on this workgroup.
-    if (rc == a.nchunk - 1 && b == a.B - 1 && grp == a.ng - 1) reduce_head(a, h, epoch);
+    //
+    // With many streams, the epoch advances once the H summing workgroups
+    // and the last workgroup of each XCD have counted (ndone of them).  A summing
+    // workgroup has seen a partial of every workgroup of its head, each
+    // published after that workgroup read the epoch, so every workgroup of
+    // the launch has read it.  The last ones of the XCDs matter when a
+    // bounded wait gives up: a summing workgroup then counts without every
+    // partial, and the advance still waits until each XCD has dispatched all
+    // its workgroups.  A few atomics on the count, not one per stream: one
+    // per stream put 768 on one word at B=48 N=512 H=16 D=64 bf16 (one chunk
+    // per stream), 45.4 us against 29.4 us.  With few streams counting each
+    // stream's first chunk before its dV pass (as the forward counts its
+    // last chunks) takes the count off the launch's tail: 0.5-2% faster.
+    if (rc == a.nchunk - 1 && b == a.B - 1 && grp == a.ng - 1)
+      reduce_head(a, h, epoch);
+    else if (!a.per_stream && item + kXcds >= (int)gridDim.x && tid == 0)
+      count_done(a.hdr, (unsigned)a.ndone, epoch);
   }
 
   // dlam[h] = the sum of head h's chunk partials in double, in a fixed order
@@ -1355,7 +1375,10 @@ struct ChunkBwd {
       }
     }
     acc = wave_sum_f64(acc);
-    if (lane == 0) a.dlam[h] = (float)acc;
+    if (lane == 0) {
+      a.dlam[h] = (float)acc;
+      if (!a.per_stream) count_done(a.hdr, (unsigned)a.ndone, epoch);
+    }
   }
 };
 
@@ -1732,6 +1755,13 @@ constexpr int kRB = 16;
 constexpr int kRBSmall = 4;
 constexpr int kNWB = 4;
 constexpr int64_t kBwdSmallGrid = 256;
+// Streams up to which every stream's first chunk counts toward the epoch's
+// advance (ChunkBwd::run).  Measured (bf16, same-box A/B, per stream / per
+// head and XCD, us): D=64 B=8 N=1024 H=6 (48 streams) 11.13 / 11.48; B=8
+// N=4096 H=12 (96) 28.77 / 29.17; B=12 N=2048 H=16 (192) 29.31 / 29.61;
+// B=16 N=2048 H=16 (256) 40.68 / 40.86; B=16 N=1024 H=16 (256) 23.96 /
+// 23.21; B=24 N=1024 H=16 (384) 37.23 / 29.21.
+constexpr int64_t kBwdPerStreamCount = 192;
 constexpr int64_t kBwdShortChainGrid = 384;
 
 // 4 rows per lane when the 16-row grid has at most kBwdSmallGrid chunks, so
@@ -2141,6 +2171,18 @@ int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides, const 
   a.f_nchunk = make_fastdiv((uint32_t)nchunk);
   a.hdr = static_cast<unsigned*>(workspace);
   a.spin_limit = spin_limit();
+  // Workgroups that count toward the epoch's advance: the H that sum a
+  // head's partials (the last row of items, chunk 0, is unrotated: item
+  // (nchunk-1)*nstream + stream with b = B-1 and the last channel group) and
+  // the last of each XCD, each counted once.
+  a.per_stream = nstream <= kBwdPerStreamCount;
+  a.ndone = (int)H;
+  for (int64_t item = grid > kXcds ? grid - kXcds : 0; item < grid; ++item) {
+    const int64_t rc = item / nstream, stream = item - rc * nstream;
+    const int64_t bh = stream / a.ng, grp = stream - bh * a.ng;
+    const bool sums = rc == nchunk - 1 && bh / H == B - 1 && grp == a.ng - 1;
+    if (!sums) ++a.ndone;
+  }
   const size_t flag_bytes = nchunk > 1 ? (size_t)(B * H * nchunk * D) * sizeof(u64) : 0;
   a.flags = nchunk > 1 ? reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes) : nullptr;
   a.partial = reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes + flag_bytes);

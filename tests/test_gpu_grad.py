@@ -98,19 +98,22 @@ def test_backward_long_sequence(hip_device, kdecay_lib, dname, H, D):
     check(dv, dl, None, rdv, rdl, None, dtype, f"N={N} D={D} {dname}")
 
 
-def test_backward_give_up_is_flagged_not_hung(hip_device, kdecay_lib):
+@pytest.mark.parametrize("B,H,N", [(2, 4, 16384), (16, 16, 1024)])
+def test_backward_give_up_is_flagged_not_hung(hip_device, kdecay_lib, B, H, N):
     """Force the backward's bounded waits (the reverse look-back and the wait
     for a head's dlam partials) to give up after one poll, through the
     library's test hook: every launch still returns and sets the workspace's
     sticky error word, the launch that gives up leaves NaN in the gradients
     it could not compute, and once the hook and the word are cleared the same
-    workspace gives finite gradients bit-identical to the first run."""
+    workspace gives finite gradients bit-identical to the first run.  8
+    streams (each stream's first chunk counts toward the epoch's advance) and
+    256 (the head-summing workgroups and the last of each XCD count)."""
     from kilat_amd.triton_ops import _stream_ptr, _workspaces
 
     g = torch.Generator().manual_seed(43)
-    lam = lam_uniform(4, 0.9, 0.9999, g)
-    V = torch.randn(2, 4, 16384, 64, generator=g).to(torch.bfloat16)  # 128 backward chunks per stream
-    gy = torch.randn(2, 4, 16384, 64, generator=g).to(torch.bfloat16)
+    lam = lam_uniform(H, 0.9, 0.9999, g)
+    V = torch.randn(B, H, N, 64, generator=g).to(torch.bfloat16)  # 128 or 2 backward chunks per stream
+    gy = torch.randn(B, H, N, 64, generator=g).to(torch.bfloat16)
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
@@ -138,6 +141,33 @@ def test_backward_give_up_is_flagged_not_hung(hip_device, kdecay_lib):
         assert kilat_amd.workspace_error(probe) == 0
     assert torch.equal(dv1, dv0) and torch.equal(dl1, dl0)
     assert bool(torch.isfinite(dv1).all()) and bool(torch.isfinite(dl1).all())
+
+
+def test_backward_epoch_counting_schemes_alternate(hip_device, kdecay_lib):
+    """One workspace, backward launches that alternate between the two ways
+    of counting toward the epoch's advance: 384 streams of 2 chunks (the
+    head-summing workgroups and the last of each XCD count), 24 streams of 6
+    (each stream's first chunk), 256 streams of 1 chunk, each against the
+    fp64 adjoint recurrence, then the first shape again, bit-identical."""
+    cases = [(24, 16, 1024), (2, 12, 3000), (16, 16, 512)]
+    data = []
+    for k, (B, H, N) in enumerate(cases):
+        g = torch.Generator().manual_seed(220 + k)
+        lam = lam_uniform(H, 0.8, 0.9999, g)
+        V = torch.randn(B, H, N, 64, generator=g).to(torch.bfloat16)
+        gy = torch.randn(B, H, N, 64, generator=g).to(torch.bfloat16)
+        data.append((lam, V, gy))
+    first = None
+    for k in (0, 1, 2, 0):
+        lam, V, gy = data[k]
+        dv, dl, _ = gpu_grads(lam, V, gy, hip_device)
+        if k == 0 and first is not None:
+            assert torch.equal(dv, first[0]) and torch.equal(dl, first[1])
+            continue
+        rdv, rdl, _ = O.scan_grads_f64(lam, V, gy)
+        check(dv, dl, None, rdv, rdl, None, torch.bfloat16, f"case {k}")
+        if k == 0:
+            first = (dv, dl)
 
 
 def test_backward_randomized(hip_device, kdecay_lib):
