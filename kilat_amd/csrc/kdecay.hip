@@ -1061,7 +1061,9 @@ struct ChunkBwd {
     // per-row guard (C2 29.5 -> 29.3 us, B=1 N=65536 H=16 D=128 146.6 ->
     // 145.2 us).  Only for full 128-byte channel groups: for narrower ones
     // the second loop made one of the kernels spill (D=32 bf16, several
-    // rounds, 7% slower).
+    // rounds, 7% slower).  With 16 rows, at most two rows' stores in flight
+    // per wavefront, as in the forward (C2 29.65 -> 29.18 us, B=24 N=1024
+    // H=16 29.63 -> 29.29 us, same-box A/B; no gain with 4 rows).
     if constexpr (LPR == 8) {
       if (li == R - 1 && fin_i < 0) {
 #pragma unroll
@@ -1073,6 +1075,9 @@ struct ChunkBwd {
 #pragma unroll
           for (int j = 0; j < VW; ++j) gn[j] = __builtin_fmaf(lam, gn[j], gv[j] * rz);
           store_vec<T, VW>(dp + (int64_t)i * a.dn, gn);
+          if constexpr (R >= 16) {
+            if (i <= R - 3) wait_vmcnt<2>();
+          }
           pin(gn);
         }
         return;
