@@ -1635,9 +1635,10 @@ int64_t chunk_rows(int v_dtype, int64_t D, ChunkShape c) {
 
 // Chunk shape of a problem: (kR, kNW), or (kRSmall, kNWSmall) when a
 // (kR, kNW) grid would leave most of the device idle: at most kSmallGrid
-// chunks, kSmallGrid2 with 2 chunks per stream (the 8-row grid, 2x the
-// workgroups, still resident at five per CU) and kSmallGrid1 with 1 (the
-// 16-row grid then needs no look-back at all, the 8-row one a chain of 2).
+// chunks, kSmallGrid2 with 2 chunks per stream (up to 1280 workgroups of 8
+// rows; just above it they lose 13-19%, measured below) and kSmallGrid1 with
+// 1 (the 16-row grid then needs no look-back at all, the 8-row one a chain of
+// 2).
 // Measured on MI355X (bf16, same-box A/B of the current kernels, 16 rows
 // against 8, us; chunks at 16 rows): D=64 N=2048 B=8, 4 per stream: H=12
 // (384) 11.62 / 10.58, H=14 (448) 11.87 / 11.96, H=16 (512) 12.46 / 12.99;
