@@ -117,9 +117,20 @@ __device__ __forceinline__ void store16_stream(void* p, unsigned a, unsigned b, 
 }
 
 // Store N floats (N = 4 or 8) as N elements of T at p (16-byte aligned).
+// Eight floats take two 16-byte stores, each of which covers every other 16
+// bytes of the row's range across the lanes: through the cache, whose lines
+// the second store completes before they are written back (non-temporal,
+// bf16 in / fp32 out at B=8 N=4096 H=12 D=64 took 52.2 us; cached, 29.7 us).
 template <typename T, int N>
 __device__ __forceinline__ void store_vec(T* p, const float* f) {
-  if constexpr (sizeof(T) == 4) {
+  if constexpr (sizeof(T) == 4 && N == 8) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const u32x4 v = {__float_as_uint(f[4 * k]), __float_as_uint(f[4 * k + 1]), __float_as_uint(f[4 * k + 2]),
+                       __float_as_uint(f[4 * k + 3])};
+      *reinterpret_cast<u32x4*>(p + 4 * k) = v;
+    }
+  } else if constexpr (sizeof(T) == 4) {
 #pragma unroll
     for (int k = 0; k < N / 4; ++k)
       store16_stream(p + 4 * k, __float_as_uint(f[4 * k]), __float_as_uint(f[4 * k + 1]),
