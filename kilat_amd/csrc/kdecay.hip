@@ -259,7 +259,9 @@ typedef unsigned long long u64;
 
 // Header words (first 256 bytes of the workspace).
 //   EPOCH  launch generation: look-back words of older launches never match
-//   DONE   streams of the running launch whose last chunk has finished
+//   DONE   workgroups of the running launch that have counted toward the
+//          epoch's advance (the forward: each stream's last chunk; the
+//          backward: see ChunkBwd::run)
 //   ERROR  sticky fault word (1: a look-back gave up waiting)
 enum { HDR_EPOCH = 0, HDR_DONE = 1, HDR_ERROR = 2 };
 constexpr size_t kHeaderBytes = 256;
