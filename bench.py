@@ -518,7 +518,7 @@ def main() -> int:
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the decay scan shards over (b, h) streams with no communication; see DESIGN.md)",
+              "(the decay scan shards over (b, h) streams with no communication)",
               file=sys.stderr, flush=True)
         return 2
     import torch

@@ -1,6 +1,6 @@
-"""The ctypes stub INTEGRATION.md shows a Kilat maintainer, kept here verbatim
-so that tests can run it (tests/test_gpu_scan.py) and check that the document
-still holds this exact text (tests/test_abi.py)."""
+"""The ctypes stub the integration guide shows a Kilat maintainer, kept here
+verbatim so that tests can run it (tests/test_gpu_scan.py) and check that the
+guide still holds this exact text (tests/test_abi.py)."""
 from __future__ import annotations
 
 STUB_SOURCE = """\

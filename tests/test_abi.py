@@ -257,13 +257,13 @@ def test_bench_refuses_more_than_one_gpu():
 
 
 def test_integration_doc_holds_the_tested_ctypes_stub():
-    """INTEGRATION.md's ctypes stub is the text tests/ctypes_stub.py runs on the GPU."""
+    """The integration guide's ctypes stub is the text tests/ctypes_stub.py runs on the GPU."""
     from tests.ctypes_stub import STUB_SOURCE
 
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     doc = os.path.join(root, "INTEGRATION.md")
     if not os.path.exists(doc):
-        pytest.skip("INTEGRATION.md is not in this copy of the tree")
+        pytest.skip("the integration guide is not in this copy of the tree")
     assert STUB_SOURCE in open(doc).read()
 
 

@@ -457,7 +457,7 @@ def test_lookback_give_up_is_flagged_not_hung(hip_device, kdecay_lib):
 
 
 def test_integration_ctypes_stub_matches_package(hip_device, kdecay_lib):
-    """The stand-alone ctypes stub of INTEGRATION.md gives the package's bits,
+    """The integration guide's stand-alone ctypes stub gives the package's bits,
     on a contiguous V and on the projection's strided (B,N,H*D) view."""
     from kilat_amd import _build
     from tests.ctypes_stub import load
