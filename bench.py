@@ -277,6 +277,46 @@ def measured_traffic():
         return None
 
 
+def bench_forward_dtypes(torch, dev, steps=100):
+    """The C2 shape (B=8 N=4096 H=12) with other I/O types than the headline's
+    bf16: fp16, fp32 in and out (D=64: two 128-byte channel groups per head, so
+    twice the bytes and 1.5 rounds; D=32: C2's bytes), and bf16 in / fp32 out.
+    Algorithmic bytes: V read once, y written once.  4 rotated sets."""
+    from kilat_amd import _lib
+    from kilat_amd.triton_ops import _stream_ptr, _workspace
+
+    B, H, N = 8, 12, 4096
+    lib = _lib.load()
+    codes = {torch.float32: _lib.KDECAY_F32, torch.bfloat16: _lib.KDECAY_BF16, torch.float16: _lib.KDECAY_F16}
+    lam = c2_lam(H, torch).to(dev)
+    stream = _stream_ptr(dev)
+    out = {}
+    for name, ti, to, D in (("f16", torch.float16, torch.float16, 64), ("f32_d64", torch.float32, torch.float32, 64),
+                            ("f32_d32", torch.float32, torch.float32, 32), ("bf16_in_f32_out", torch.bfloat16,
+                                                                             torch.float32, 64)):
+        g = torch.Generator(device=dev).manual_seed(11)
+        sets = [(torch.randn(B, H, N, D, generator=g, device=dev).to(ti), torch.empty(B, H, N, D, device=dev, dtype=to))
+                for _ in range(4)]
+        nb = lib.kdecay_scan_workspace_bytes(B, H, N, D, codes[ti])
+        ws = _workspace(dev, stream, nb)
+        args = [(V.data_ptr(), codes[ti], _lib.strides4(V.stride()), y.data_ptr(), codes[to], _lib.strides4(y.stride()),
+                 lam.data_ptr(), None, None, B, H, N, D, 0, ws.data_ptr(), ws.numel(), stream) for V, y in sets]
+        rc = [0]
+
+        def launch(k, args=args, rc=rc):
+            rc[0] |= lib.kdecay_scan_fwd(*args[k % len(args)])
+
+        region, _ = time_region(torch, launch, steps, 200, events=False)
+        if rc[0]:
+            raise RuntimeError("scan failed: " + lib.kdecay_last_error_string().decode())
+        us = region * 1e3 / steps
+        nbytes = B * H * N * D * (sets[0][0].element_size() + sets[0][1].element_size())
+        out[name] = {"D": D, "us": round(us, 3), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "pct_of_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 2)}
+        del sets, args
+    return out
+
+
 def bench_backward(torch, dev, steps=100):
     """C2-shaped training pass: kdecay_scan_fwd_train, then kdecay_scan_bwd (dV, dlam).
 
@@ -584,6 +624,9 @@ def main() -> int:
         extras["decode_layers"] = bench_decode_layers(torch, kilat_amd, dev)
         log("long context C4")
         extras["long_context"] = bench_long(torch, kilat_amd, dev)
+        torch.cuda.empty_cache()
+        log("forward with other I/O types (C2 shape)")
+        extras["forward_dtypes"] = bench_forward_dtypes(torch, dev)
         torch.cuda.empty_cache()
         log("training forward + backward (C2 shape)")
         extras["backward"] = bench_backward(torch, dev)
