@@ -438,8 +438,10 @@ def decay_path_per_layer(torch, dev, reps=200):
              _lib.strides4(y.stride()), lam.data_ptr(), None, None, B, H, N, D, 0, ws.data_ptr(), ws.numel(), stream)
             for c, y in zip(conts, ys)]
 
+    rc = [0]
+
     def scan_only(k):
-        lib.kdecay_scan_fwd(*args[k % 16])
+        rc[0] |= lib.kdecay_scan_fwd(*args[k % 16])
 
     res = {"config": "one layer at C5: B=8 N=1024 H=6 D=64 bf16, GPU-bound back-to-back, 16 rotated buffers"}
     for name, fn in (("reference_glue", glue), ("fused_layout", fused), ("scan_only_c_abi", scan_only)):
@@ -455,6 +457,9 @@ def decay_path_per_layer(torch, dev, reps=200):
             with torch.cuda.graph(g, stream=side):
                 for k in range(reps):
                     fn(k)
+        # the eager warm-up launches and the captured ones were all accepted
+        if rc[0]:
+            raise RuntimeError("kdecay_scan_fwd failed: " + lib.kdecay_last_error_string().decode())
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()

@@ -80,13 +80,19 @@ enum {
  *                so the workspace needs no clearing between launches (also
  *                under stream capture and graph replay), but it must not be
  *                shared by two launches that can run at the same time (use
- *                one per stream).  A non-zero error word (header word 2: a
- *                look-back gave up waiting) stays set until the caller
- *                zeroes the workspace.  Outputs that launch could not
- *                compute (the rows of a chunk whose look-back gave up, and
- *                any later rows or final state whose carry came through that
- *                chunk) are written as NaN, never as finite wrong values.
- *                It may be NULL when
+ *                one per stream).  A non-zero error word (header word 1,
+ *                bytes 4-7: a look-back gave up waiting) stays set until the
+ *                caller zeroes the whole workspace.  Outputs the launch that
+ *                gave up could not compute (the rows of a chunk whose
+ *                look-back gave up, and any later rows or final state whose
+ *                carry came through that chunk) are written as NaN, never as
+ *                finite wrong values.  While the word is set, every later
+ *                launch on that workspace writes NaN to all its outputs (out
+ *                and final_state) without waiting on anything: the launch
+ *                that gave up may have left look-back words tagged as a later
+ *                launch's, so only a zeroed workspace computes again.  (A
+ *                launch of one chunk per stream uses no workspace and is not
+ *                affected.)  It may be NULL when
  *                kdecay_scan_workspace_bytes() returns 0.
  *
  * Requirements of this (vector) path: D = 16, 32, or a multiple of 64 (bf16,
@@ -121,16 +127,21 @@ size_t kdecay_scan_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D,
  *   - Shapes whose kdecay_scan_workspace_bytes() exceeds
  *     KDECAY_NOALLOC_WORKSPACE_BYTES (about 16K chunks: 1 GiB of bf16 V) are
  *     rejected with KDECAY_EWORKSPACE before anything is launched.
- *   - The first call on a GPU looks the array up and enqueues its one-time
- *     clear (a fill kernel) on `stream`, ahead of the scan.
+ *   - The array is zero-filled when the library's code object is loaded on
+ *     a GPU; the first call only looks its address up (nothing is launched
+ *     or recorded for it, also under stream capture), and nothing clears it
+ *     again.
  *   - Every call on one GPU in a process shares that GPU's array (each
  *     process has its own): calls that can overlap on one GPU (two streams,
  *     two threads) race and give wrong results; serialise them, e.g. on one
  *     stream.  The array keeps the last call's contents (launch epoch and
  *     look-back words), which the next call needs no clearing for.
  *   - A look-back give-up leaves NaN in the outputs it could not compute, as
- *     kdecay_scan_fwd does; the sticky error word lives in the array and is
- *     not readable through this API.
+ *     kdecay_scan_fwd does, and sets the sticky error word in the array.
+ *     That word is not readable through this API and the array is never
+ *     cleared: from then on every call of this entry point on that GPU in the
+ *     process that needs a workspace (several chunks per stream) writes NaN
+ *     to all its outputs, which a caller checking for finite outputs sees.
  * Every other argument as kdecay_scan_fwd.
  */
 int kdecay_scan_fwd_noalloc(const void* V, int v_dtype,
@@ -191,10 +202,12 @@ size_t kdecay_scan_saved_states_floats(int64_t B, int64_t H, int64_t N,
  *
  *   V, gy, dV    [B,H,N,D] of v_dtype (gy and dV share V's dtype), strided as
  *                kdecay_scan_fwd's V; the row strides of V and gy must not
- *                be negative, and one backward chunk of rows (512 rows, or
- *                128 for grids of at most 256 such chunks) must span less
+ *                be negative, and one backward chunk of rows must span less
  *                than 2^31 bytes (rows are addressed by 32-bit offsets), else
- *                KDECAY_ELAYOUT
+ *                KDECAY_ELAYOUT.  A chunk is 4 wavefronts x (64 / lanes per
+ *                row) x 16 rows: 512 rows for a 128-byte channel group (D >=
+ *                64 bf16/fp16, D >= 32 fp32), 1024 for 64 bytes, 2048 for 32
+ *                bytes; a quarter of that for small grids.
  *   lam, init_state, t_offset   as given to the forward call
  *   states       the forward call's states (NULL allowed when
  *                kdecay_scan_saved_states_floats() is 0)
@@ -206,7 +219,9 @@ size_t kdecay_scan_saved_states_floats(int64_t B, int64_t H, int64_t N,
  *                zeroed once; same rules as kdecay_scan_fwd's (it may be the
  *                same buffer when large enough).  A bounded wait that gives
  *                up sets the error word and leaves NaN in the gradients it
- *                could not compute (dV rows, the head's dlam).
+ *                could not compute (dV rows, the head's dlam).  While the
+ *                word is set, every later backward on that workspace writes
+ *                NaN to all of dV, dlam and d_init, as the forward does.
  */
 int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides,
                     const void* gy, const int64_t* gy_strides, void* dV,

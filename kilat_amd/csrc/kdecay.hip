@@ -260,12 +260,23 @@ typedef unsigned long long u64;
 
 // Header words (first 256 bytes of the workspace).
 //   EPOCH  launch generation: look-back words of older launches never match
+//   ERROR  sticky fault word (1: a bounded wait gave up).  Every launch reads
+//          it with the epoch (one 64-bit load) and, when it is set, writes
+//          NaN to all its outputs instead of trusting the workspace: after a
+//          give-up, words of the launch that gave up may carry a later
+//          launch's tag, so only a cleared workspace computes again.
 //   DONE   workgroups of the running launch that have counted toward the
 //          epoch's advance (the forward: each stream's last chunk; the
 //          backward: see ChunkBwd::run)
-//   ERROR  sticky fault word (1: a look-back gave up waiting)
-enum { HDR_EPOCH = 0, HDR_DONE = 1, HDR_ERROR = 2 };
+enum { HDR_EPOCH = 0, HDR_ERROR = 1, HDR_DONE = 2 };
 constexpr size_t kHeaderBytes = 256;
+
+// The epoch and the error word of a workspace header, as one load.
+struct EpochErr {
+  unsigned epoch, err;
+};
+
+__device__ __forceinline__ EpochErr split_header(u64 w) { return EpochErr{(unsigned)w, (unsigned)(w >> 32)}; }
 
 // Tag of a word published in launch `epoch`: kind 0 = aggregate, 1 = inclusive.
 // Zeroed memory (tag 0) never matches a live tag.
@@ -509,10 +520,11 @@ __device__ __forceinline__ void count_done(unsigned* hdr, unsigned n, unsigned e
   }
 }
 
-__device__ __forceinline__ unsigned read_epoch_v(const unsigned* hdr) {
+__device__ __forceinline__ EpochErr read_epoch_v(const unsigned* hdr) {
   unsigned zero;
   asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
-  return __hip_atomic_load(const_cast<unsigned*>(hdr) + HDR_EPOCH + zero, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return split_header(__hip_atomic_load(reinterpret_cast<u64*>(const_cast<unsigned*>(hdr)) + zero, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT));
 }
 
 // Keeps `x` opaque to the optimiser at this point, so values derived from it
@@ -634,12 +646,12 @@ struct ChunkScan {
     return lam;
   }
 
-  // Scan `item` from its loaded rows and store its outputs.  `epoch` is the
-  // launch generation every workgroup read before publishing anything.
-  // Tables, chunk reduction and look-back: st = the state before this lane's
-  // first row.
+  // Scan `item` from its loaded rows and store its outputs.  `eh` holds the
+  // launch generation every workgroup read before publishing anything and
+  // the workspace's sticky error word.  Tables, chunk reduction and
+  // look-back: st = the state before this lane's first row.
   __device__ static void scan_chunk(const ScanArgs& a, const Pos& p, uint4 (&raw)[R], float lam, float init,
-                                    unsigned epoch, Smem& sm, float (&st)[VW]) {
+                                    EpochErr eh, Smem& sm, float (&st)[VW]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const bool multi = a.nchunk > 1;
     const int chunk = p.chunk, stream = p.stream;
@@ -687,9 +699,17 @@ struct ChunkScan {
 
     // Carry into the chunk: wavefront 0 publishes and looks back.
     const float mW = sm.pw[GW];
+    // A workspace whose error word is set may hold words tagged for this
+    // launch by the launch that gave up: wavefront 0 then takes the carry as
+    // NaN (every output of the chunk, its inclusive word and through it the
+    // later chunks become NaN), waits for nothing and does not count toward
+    // the epoch's advance (so the epoch every workgroup reads stays the same
+    // and no poisoned launch waits for words it will never see).
+    bool poisoned = false;
     if (wave == 0) {
       const float mL = sm.pw[G];
-      const unsigned tag_agg = tag_of(epoch, 0u), tag_inc = tag_of(epoch, 1u);
+      const unsigned tag_agg = tag_of(eh.epoch, 0u), tag_inc = tag_of(eh.epoch, 1u);
+      poisoned = __builtin_amdgcn_readfirstlane(eh.err) != 0;
       u64* base = multi ? a.flags + (int64_t)stream * a.nchunk * DG : nullptr;
       float agg[DQ], carry[DQ];
 #pragma unroll
@@ -704,7 +724,12 @@ struct ChunkScan {
           if (chunk > 0 && !last) publish(base + (int64_t)chunk * DG + d, tag_agg, agg[q]);
         }
       }
-      if (chunk > 0) look_back<W, DG, DQ>(base, chunk, tag_agg, tag_inc, mL, a.hdr, a.spin_limit, carry);
+      if (poisoned) {
+#pragma unroll
+        for (int q = 0; q < DQ; ++q) carry[q] = __builtin_nanf("");
+      } else if (chunk > 0) {
+        look_back<W, DG, DQ>(base, chunk, tag_agg, tag_inc, mL, a.hdr, a.spin_limit, carry);
+      }
 #pragma unroll
       for (int q = 0; q < DQ; ++q) {
         const int d = lane + 64 * q;
@@ -722,7 +747,7 @@ struct ChunkScan {
     // workgroup of this launch has read the epoch (each holds at least one
     // item): advance it for the next launch.  (Counted after the stores
     // instead, C2 measured 1.7% slower and the small grids 2.5%.)
-    if (multi && last && tid == 0) count_done(a.hdr, (unsigned)a.nstream, epoch);
+    if (multi && last && tid == 0 && !poisoned) count_done(a.hdr, (unsigned)a.nstream, eh.epoch);
 
     // The lane's true start state.
     float ew[VW];  // state before this wavefront's first row, zero carry into the chunk
@@ -846,18 +871,19 @@ struct ChunkScan {
   }
 
   __device__ static void process(const ScanArgs& a, const Pos& p, uint4 (&raw)[R], float lam, float init,
-                                 unsigned epoch, Smem& sm) {
+                                 EpochErr eh, Smem& sm) {
     float st[VW];
-    scan_chunk(a, p, raw, lam, init, epoch, sm, st);
+    scan_chunk(a, p, raw, lam, init, eh, sm, st);
     store_chunk(a, p, raw, lam, st, sm);
   }
 };
 
-// The launch epoch, read by every thread before it loads any rows (so that
-// waiting for it does not wait for them).
-__device__ __forceinline__ unsigned read_epoch(const ScanArgs& a) {
-  if (a.nchunk <= 1) return 0u;
-  return __hip_atomic_load(a.hdr + HDR_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// The launch epoch and the error word, read by every thread before it loads
+// any rows (so that waiting for them does not wait for the rows).  A launch
+// of one chunk per stream has no workspace.
+__device__ __forceinline__ EpochErr read_epoch(const ScanArgs& a) {
+  if (a.nchunk <= 1) return EpochErr{0u, 0u};
+  return split_header(__hip_atomic_load(reinterpret_cast<u64*>(a.hdr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 
 // One item per workgroup: workgroup b owns item b.  An item only waits on
@@ -869,12 +895,12 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, 8)
 void scan_chunked(ScanArgs a) {
   using CS = ChunkScan<TI, TO, LPR, R, NW, W, FZ, THR>;
   __shared__ typename CS::Smem sm;
-  const unsigned epoch = read_epoch(a);
+  const EpochErr eh = read_epoch(a);
   const Pos p = pos_of(a, (int)blockIdx.x);
   uint4 raw[R];
   float init;
   const float lam = CS::load(a, p, raw, init);
-  CS::process(a, p, raw, lam, init, epoch, sm);
+  CS::process(a, p, raw, lam, init, eh, sm);
 }
 
 // --------------------------------------------------------------------------
@@ -1237,7 +1263,8 @@ struct ChunkBwd {
     // every row has been consumed: loads complete in order, so waiting for it
     // earlier would have waited for every row (and holding it in a register
     // across the row loads would spill).
-    const unsigned epoch = read_epoch_v(a.hdr);
+    const EpochErr eh = read_epoch_v(a.hdr);
+    const unsigned epoch = eh.epoch;
     if (!kFold) sweep_gy(rg, g, fin_i, ds, sm, qz, ra);
 
     // Scans over the row groups of the wavefront, both directions: sl holds
@@ -1266,6 +1293,7 @@ struct ChunkBwd {
     // (wavefront 0, first: later chunks wait on its inclusive word).
     const float mW = sm.pw[GW];
     float cg[DQ];
+    bool poisoned = false;  // wavefront 0: the workspace's error word is set
     if (wave == 0) {
       const float mL = sm.pw[G];
       const unsigned tag_agg = tag_of(epoch, 0u), tag_inc = tag_of(epoch, 1u);
@@ -1282,7 +1310,18 @@ struct ChunkBwd {
           if (rc > 0 && chunk > 0) publish(base + (int64_t)rc * DG + d, tag_agg, agg[q]);
         }
       }
-      if (rc > 0) look_back<W, DG, DQ>(base, rc, tag_agg, tag_inc, mL, a.hdr, a.spin_limit, cg);
+      // As in the forward: with the workspace's error word set, the carry is
+      // NaN, nothing is waited for and nothing counts toward the epoch's
+      // advance (dV, d(init) and the chunk's dlam partial, hence the head's
+      // dlam, become NaN; every partial is still published, under the one
+      // epoch all workgroups read, so the head sums do not wait either).
+      poisoned = __builtin_amdgcn_readfirstlane(eh.err) != 0;
+      if (poisoned) {
+#pragma unroll
+        for (int q = 0; q < DQ; ++q) cg[q] = __builtin_nanf("");
+      } else if (rc > 0) {
+        look_back<W, DG, DQ>(base, rc, tag_agg, tag_inc, mL, a.hdr, a.spin_limit, cg);
+      }
 #pragma unroll
       for (int q = 0; q < DQ; ++q) {
         const int d = lane + 64 * q;
@@ -1352,7 +1391,7 @@ struct ChunkBwd {
 
     // Few streams: the first chunk of each stream counts, as soon as its
     // look-back is done (see the end of run()).
-    if (a.per_stream && chunk == 0 && tid == 0) count_done(a.hdr, (unsigned)a.nstream, epoch);
+    if (a.per_stream && chunk == 0 && tid == 0 && !poisoned) count_done(a.hdr, (unsigned)a.nstream, epoch);
 
     // dV with the true carry.
     float gn[VW];
@@ -1382,8 +1421,8 @@ struct ChunkBwd {
     // stream's first chunk before its dV pass (as the forward counts its
     // last chunks) takes the count off the launch's tail: 0.5-2% faster.
     if (rc == a.nchunk - 1 && b == a.B - 1 && grp == a.ng - 1)
-      reduce_head(a, h, epoch);
-    else if (!a.per_stream && item + kXcds >= (int)gridDim.x && tid == 0)
+      reduce_head(a, h, epoch, poisoned);
+    else if (!a.per_stream && item + kXcds >= (int)gridDim.x && tid == 0 && !poisoned)
       count_done(a.hdr, (unsigned)a.ndone, epoch);
   }
 
@@ -1391,7 +1430,7 @@ struct ChunkBwd {
   // whatever the order in which they arrive (deterministic): wavefront 0
   // alone, each lane summing a strided subset (all its reads issued at
   // once), then a fixed butterfly across the lanes.
-  __device__ static void reduce_head(const BwdArgs& a, int h, unsigned epoch) {
+  __device__ static void reduce_head(const BwdArgs& a, int h, unsigned epoch, bool poisoned) {
     if (threadIdx.x >= 64) return;
     const int lane = threadIdx.x;
     const unsigned tag = tag_of(epoch, 0u);
@@ -1427,7 +1466,7 @@ struct ChunkBwd {
     acc = wave_sum_f64(acc);
     if (lane == 0) {
       a.dlam[h] = (float)acc;
-      if (!a.per_stream) count_done(a.hdr, (unsigned)a.ndone, epoch);
+      if (!a.per_stream && !poisoned) count_done(a.hdr, (unsigned)a.ndone, epoch);
     }
   }
 };
@@ -1567,10 +1606,6 @@ __global__ __launch_bounds__(256) void decay_step4(StepArgs a) {
   }
   store4<float>(a.s_out + idx, ns);
   store4<TO>(static_cast<TO*>(a.out) + idx, o);
-}
-
-__global__ __launch_bounds__(256) void zero_words(unsigned long long* p, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = 0ull;
 }
 
 __global__ __launch_bounds__(256) void zero_floats(float* p, int64_t n) {
@@ -1937,9 +1972,12 @@ int empty_final_state(const float* init, float* fin, int64_t n, hipStream_t s) {
 // Look-back workspace of kdecay_scan_fwd_noalloc: a fixed array in the code
 // object's device memory, so that entry point allocates nothing.  Each GPU the
 // library is loaded on holds its own copy, at its own address, until the
-// process ends.  On the host this name is only a stand-in for the symbol, not
-// a device address: host code uses the address hipGetSymbolAddress returns
-// for the current device (scratch_of_current_device), never `scratch` itself.
+// process ends.  It has no initialiser, so the loader zero-fills it when the
+// code object is loaded on a device (a zeroed workspace is what the epoch
+// protocol starts from); the library never clears it again.  On the host this
+// name is only a stand-in for the symbol, not a device address: host code
+// uses the address hipGetSymbolAddress returns for the current device
+// (scratch_of_current_device), never `scratch` itself.
 static __device__ __align__(256) unsigned char scratch[KDECAY_NOALLOC_WORKSPACE_BYTES];
 
 namespace kd {
@@ -1949,12 +1987,11 @@ std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device (null until set up)
 
 // Device address of the current device's scratch array.  The first call on a
-// device looks the address up (hipGetSymbolAddress, with that device current)
-// and clears the array once with a fill kernel on `s`, ahead of the caller's
-// launch (a kernel rather than hipMemsetAsync, so that a first call under
-// stream capture records a kernel node; replaying that clear is harmless).
-// Later calls find the epoch protocol's state in place.
-int scratch_of_current_device(hipStream_t s, void** p) {
+// device looks the address up (hipGetSymbolAddress, with that device current);
+// nothing is launched or recorded for it, so a first call under stream
+// capture records only the scan.  Later calls find the epoch protocol's state
+// in place.
+int scratch_of_current_device(void** p) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return fail((int)e, "hipGetDevice: %s", hipGetErrorString(e));
@@ -1965,10 +2002,6 @@ int scratch_of_current_device(hipStream_t s, void** p) {
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return fail((int)e, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
     if (!ptr) return fail(KDECAY_EINVAL, "hipGetSymbolAddress(scratch) returned a null address");
-    hipLaunchKernelGGL(zero_words, dim3(1024), dim3(256), 0, s, static_cast<u64*>(ptr),
-                       (int64_t)(KDECAY_NOALLOC_WORKSPACE_BYTES / sizeof(u64)));
-    const int rc = hip_check("scratch clear launch");
-    if (rc) return rc;
     g_scratch_ptr[dev] = ptr;
   }
   *p = g_scratch_ptr[dev];
@@ -2101,7 +2134,7 @@ int kdecay_scan_fwd_noalloc(const void* V, int v_dtype, const int64_t* v_strides
                 need, (size_t)KDECAY_NOALLOC_WORKSPACE_BYTES);
   void* ws = nullptr;
   if (need) {
-    const int e = scratch_of_current_device(static_cast<hipStream_t>(stream), &ws);
+    const int e = scratch_of_current_device(&ws);
     if (e) return e;
   }
   return scan_fwd_impl(V, v_dtype, v_strides, out, out_dtype, out_strides, lam, init_state, final_state, B, H, N, D,

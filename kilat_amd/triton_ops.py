@@ -90,6 +90,22 @@ def _vector_layout_ok(t: torch.Tensor) -> bool:
             and (st[0] % vw == 0 or sz[0] == 1))
 
 
+def _bwd_rows_fit(t: torch.Tensor) -> bool:
+    """The backward kernel's addressing rule: it reads one chunk of rows of V
+    and of the upstream gradient through 32-bit byte offsets, so a chunk's
+    rows must span less than 2^31 bytes (the library rejects other row
+    strides).  A chunk holds at most 4 wavefronts x (64 lanes / lanes per
+    row) x 16 rows per lane; the bound below uses that largest chunk, so a
+    tensor that passes is accepted whatever chunk size the library picks."""
+    B, H, N, D = t.shape
+    es = t.element_size()
+    lanes_per_row = min(D, 128 // es) * es // 16
+    if N <= 1 or lanes_per_row < 1:
+        return True
+    max_rows = 4 * (64 // lanes_per_row) * 16
+    return max_rows * t.stride(2) * es <= 0x7FFFFFFF
+
+
 if hasattr(torch._C, "_cuda_getCurrentRawStream"):
     def _stream_ptr(device: torch.device) -> int:
         """The raw handle of torch's current stream on `device`."""
@@ -170,14 +186,18 @@ def workspace_error(V: torch.Tensor, clear: bool = False) -> int:
     """Sticky error word of the workspace used for V's device and current stream.
 
     0: no fault.  1: a bounded wait of some earlier launch gave up (a
-    look-back, or the backward's wait for a head's dlam partials): that
-    launch's output is wrong.  clear=True zeroes the whole workspace after
-    reading it (the word stays set until then).  Synchronises the stream.
+    look-back, or the backward's wait for a head's dlam partials).  The launch
+    that gave up wrote NaN where it could not compute, and while the word is
+    set every later launch on this workspace writes NaN to all its outputs
+    (y, the final state, dV, dlam, d(init)): the workspace may hold words of
+    that launch tagged as a later launch's, so only a cleared workspace
+    computes again.  clear=True zeroes the whole workspace after reading it.
+    Synchronises the stream.
     """
     ws = _workspaces.get((V.device.index, _stream_ptr(V.device)))
     if ws is None:
         return 0
-    err = int(ws[8:12].view(torch.int32).item())
+    err = int(ws[4:8].view(torch.int32).item())
     if err and clear:
         ws.zero_()
     return err
@@ -210,7 +230,9 @@ class _ScanFn(torch.autograd.Function):
         dev = V.device
         v_code = _DTYPE_CODE[V.dtype]
         o_code = _DTYPE_CODE[out_dtype]
-        Vk = V if _vector_layout_ok(V) else V.contiguous()
+        # The saved V also feeds the backward kernel, whose addressing takes
+        # a narrower range of row strides than the forward's.
+        Vk = V if _vector_layout_ok(V) and _bwd_rows_fit(V) else V.contiguous()
         out = torch.empty(Vk.shape, dtype=out_dtype, device=dev) if out_dtype != Vk.dtype else torch.empty_like(Vk)
         if not _vector_layout_ok(out):
             out = torch.empty(Vk.shape, dtype=out_dtype, device=dev)
@@ -254,7 +276,7 @@ class _ScanFn(torch.autograd.Function):
         if gy is None:
             gy = torch.zeros_like(Vk)
         gy = gy.to(Vk.dtype)
-        if not _vector_layout_ok(gy):
+        if not (_vector_layout_ok(gy) and _bwd_rows_fit(gy)):
             gy = gy.contiguous()
         dV = torch.empty_like(Vk)
         if not _vector_layout_ok(dV):

@@ -19,6 +19,13 @@ Fixture: ids [2,16] int64, logits [2,16,256] float32, loss, weight checksum,
 and the configuration.  Reference files exercised: model.py:191-257 and
 :490-595, blocks.py:80-90 and :306-406, attention.py:146-518,
 ffn.py:63-112, :232-367 and :403-482, triton_ops.py:232-330.
+
+The decode cache, as the generation loop drives it (generation_mixin.py:
+484-509): a prefill of the first INC_PREFILL tokens with use_cache=True, then
+one call per later token with the returned past_key_values (the incremental
+path, attention.py:310-360 and :434-491): inc_prefill_logits [2,12,256],
+inc_step_logits [4,2,1,256], and inc_states [2 layers, 2, 2, 16], every
+layer's decay state after the last step.
 """
 from __future__ import annotations
 
@@ -39,6 +46,28 @@ OUT = os.path.join(HERE, "c5_tiny_golden.npz")
 SEED = 1234
 CFG = dict(vocab_size=256, n_embd=64, n_layer=2, n_head=4, recall_ratio=0.5, num_experts=4, active_experts=2)
 B, N = 2, 16
+INC_PREFILL = 12  # tokens of the cached prefill; the other N - INC_PREFILL are decoded one at a time
+
+
+def run_with_cache(model, ids, reference: bool):
+    """Prefill ids[:, :INC_PREFILL] with use_cache, then one call per later
+    token with the cache: (prefill logits, [step logits], decay states of
+    every layer after the last step)."""
+    def call(x, past):
+        if reference:
+            out = model(x, past_key_values=past, use_cache=True, return_dict=True)
+            return out.logits.float(), out.past_key_values
+        logits, _, presents = model(x, past_key_values=past, use_cache=True)
+        return logits.float(), presents
+
+    with torch.no_grad():
+        pre, past = call(ids[:, :INC_PREFILL], None)
+        steps = []
+        for t in range(INC_PREFILL, ids.shape[1]):
+            lg, past = call(ids[:, t:t + 1], past)
+            steps.append(lg)
+    states = torch.stack([layer[0].float() for layer in past])
+    return pre, torch.stack(steps), states
 
 
 def weight_checksum(model: torch.nn.Module) -> float:
@@ -105,10 +134,15 @@ def main() -> None:
     logits = out.logits.float()
     print(f"reference loss {float(out.loss):.6f}; restatement loss {float(mine_loss):.6f}; "
           f"max |logit diff| {float((mine - logits).abs().max()):.3e} (scale {float(logits.abs().max()):.3e})")
+    pre, steps, states = run_with_cache(ref, ids, reference=True)
+    m_pre, m_steps, m_states = run_with_cache(ours, ids, reference=False)
+    print(f"with the cache: prefill max |diff| {float((m_pre - pre).abs().max()):.3e}, steps "
+          f"{float((m_steps - steps).abs().max()):.3e}, states {float((m_states - states).abs().max()):.3e}")
     np.savez_compressed(
         OUT, ids=ids.numpy(), logits=logits.numpy(), loss=np.float64(float(out.loss)),
         weight_checksum=np.float64(weight_checksum(ours)), seed=np.int64(SEED),
         config=np.array(repr(sorted(CFG.items()))),
+        inc_prefill_logits=pre.numpy(), inc_step_logits=steps.numpy(), inc_states=states.numpy(),
     )
     print(f"wrote {OUT}")
 

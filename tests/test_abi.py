@@ -154,6 +154,49 @@ def test_backward_rejects_bad_arguments(kdecay_lib):
     assert _bwd(lib, ws=FAKE + 16) == _lib.KDECAY_EWORKSPACE  # not 256-byte aligned
 
 
+def test_backward_row_stride_predicate_of_the_shim(kdecay_lib):
+    """The shim's _bwd_rows_fit (which sends V and the upstream gradient to
+    the backward kernel as they lie, or as contiguous copies) never passes a
+    row stride the library's backward refuses: for bf16 D=64 (512-row chunks
+    at most), bf16 D=32 (1024) and bf16 D=16 (2048), every stride it accepts
+    gets past the library's layout check (the call then stops at the missing
+    workspace, before any HIP call), and strides just above its bound are
+    refused by the library with KDECAY_ELAYOUT where the library uses that
+    largest chunk."""
+    from kilat_amd.triton_ops import _bwd_rows_fit
+
+    class Strided:  # shape, strides and element size of a [B,H,N,D] bf16 view, no memory
+        def __init__(self, shape, row_stride):
+            self.shape = shape
+            self._st = (shape[1] * shape[2] * row_stride, shape[2] * row_stride, row_stride, 1)
+
+        def stride(self, k):
+            return self._st[k]
+
+        def element_size(self):
+            return 2
+
+    lib = kdecay_lib
+    B, H, N = 8, 12, 16384  # 8 or more chunks per stream: the library takes its largest chunks
+    for D, rows in ((64, 512), (32, 1024), (16, 2048)):
+        limit = 0x7FFFFFFF // (rows * 2)
+        for S in (D, 4096, limit - 64, limit, limit + 1, limit + 64, 1 << 22):
+            S = S // 8 * 8  # keep every row 16-byte aligned
+            if S < D:
+                continue
+            t = Strided((B, H, N, D), S)
+            vstr = (H * N * S, N * S, S, 1)
+            rc = lib.kdecay_scan_bwd(FAKE, _lib.KDECAY_BF16, _lib.strides4(vstr), FAKE, _lib.strides4(vstr), FAKE,
+                                     _lib.strides4((H * N * D, N * D, D, 1)), FAKE, None, FAKE, None, FAKE, None,
+                                     B, H, N, D, 0, None, 0, None)
+            if _bwd_rows_fit(t):
+                assert rc == _lib.KDECAY_EWORKSPACE, (D, S, rc)
+            else:
+                assert rc == _lib.KDECAY_ELAYOUT, (D, S, rc)
+    # one row per stream: no chunk spans anything
+    assert _bwd_rows_fit(Strided((1, 1, 1, 64), 1 << 40))
+
+
 def test_noalloc_scan_rejects_oversized_and_bad_arguments(kdecay_lib):
     """The allocation-free entry point checks its arguments, and that the
     shape's workspace fits its fixed device array, before it touches the

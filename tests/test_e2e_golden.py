@@ -21,12 +21,12 @@ from oracle import decay_oracle as O
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "c5_tiny_golden.npz")
 
 
-def _restatement(decay):
+def _restatement(decay, cache_ops=None):
     from tests.golden.make_c5_golden import CFG, SEED, weight_checksum
     from tests.e2e_model import E2EConfig, KilatE2E
 
     torch.manual_seed(SEED)
-    model = KilatE2E(E2EConfig(**CFG), decay).eval()
+    model = KilatE2E(E2EConfig(**CFG), decay, cache_ops=cache_ops).eval()
     with torch.no_grad():
         g = torch.Generator().manual_seed(SEED + 1)
         for blk in model.layers:
@@ -68,3 +68,47 @@ def test_restatement_on_gpu_with_hip_decay_matches_reference_logits(hip_device, 
         print(f"  fused_layout={fused}: logits rel err {err:.3e}", flush=True)
         assert err <= 1e-4, f"fused={fused}: logits rel err {err:.3e}"
         assert float(loss) == pytest.approx(float(d["loss"]), rel=1e-4)
+
+
+def test_restatement_cache_path_matches_reference_on_cpu():
+    """The decode cache as the reference's generation loop drives it: a
+    prefill with use_cache (the decay state seeded by attention.py:383-394),
+    then one token per call through the incremental path (attention.py:
+    344-360, t_pos = the latent cache's length).  The restatement with the
+    reference's torch operations gives the reference model's own logits of
+    every call and every layer's final decay state, bit for bit."""
+    from tests.e2e_model import ReferenceDecayCache
+    from tests.golden.make_c5_golden import run_with_cache
+
+    d = np.load(GOLDEN)
+    model, _ = _restatement(O.global_decay, ReferenceDecayCache())
+    pre, steps, states = run_with_cache(model, torch.from_numpy(d["ids"]), reference=False)
+    assert torch.equal(pre, torch.from_numpy(d["inc_prefill_logits"]))
+    assert torch.equal(steps, torch.from_numpy(d["inc_step_logits"]))
+    assert torch.equal(states, torch.from_numpy(d["inc_states"]))
+
+
+@pytest.mark.gpu
+def test_restatement_cache_path_on_gpu_with_hip_kernels(hip_device, kdecay_lib):
+    """The same prefill and decode calls on the GPU, the decay path on the HIP
+    kernels (the prefill's state from the scan's final state, each token's
+    update one decay_step launch), both layouts, against the reference
+    model's logits and decay states (fp32)."""
+    import kilat_amd
+    from tests.e2e_model import KernelDecayCache
+    from tests.golden.make_c5_golden import run_with_cache
+
+    d = np.load(GOLDEN)
+    model, _ = _restatement(kilat_amd.triton_global_decay, KernelDecayCache())
+    model = model.to(hip_device)
+    ids = torch.from_numpy(d["ids"]).to(hip_device)
+    for fused in (False, True):
+        model.set_decay(kilat_amd.triton_global_decay, fused_layout=fused)
+        pre, steps, states = run_with_cache(model, ids, reference=False)
+        torch.cuda.synchronize()
+        for name, got in (("inc_prefill_logits", pre), ("inc_step_logits", steps), ("inc_states", states)):
+            ref = torch.from_numpy(d[name])
+            err = float((got.cpu() - ref).abs().max() / ref.abs().max())
+            print(f"  fused_layout={fused} {name}: rel err {err:.3e}", flush=True)
+            assert err <= 1e-4, f"fused={fused} {name}: rel err {err:.3e}"
+

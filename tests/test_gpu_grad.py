@@ -100,16 +100,17 @@ def test_backward_long_sequence(hip_device, kdecay_lib, dname, H, D):
 
 @pytest.mark.parametrize("B,H,N", [(2, 4, 16384), (16, 16, 1024)])
 def test_backward_give_up_is_flagged_not_hung(hip_device, kdecay_lib, B, H, N):
-    """Force the backward's bounded waits (the reverse look-back and the wait
-    for a head's dlam partials) to give up after one poll, through the
-    library's test hook: every launch still returns and sets the workspace's
-    sticky error word, the launch that gives up leaves NaN in the gradients
-    it could not compute, and once the hook and the word are cleared the same
-    workspace gives finite gradients bit-identical to the first run.  8
-    streams (each stream's first chunk counts toward the epoch's advance) and
-    256 (the head-summing workgroups and the last of each XCD count)."""
-    from kilat_amd.triton_ops import _stream_ptr, _workspaces
-
+    """Force the bounded waits (the training forward's look-back, the
+    backward's reverse look-back and its wait for a head's dlam partials) to
+    give up after one poll, through the library's test hook: every launch
+    still returns and sets the workspace's sticky error word, and the launch
+    that gives up leaves NaN in the gradients it could not compute.  From then
+    on the workspace is poisoned: the next training pass on it, with the
+    normal poll limit again, gives NaN for every element of dV and for every
+    head's dlam, until the workspace is cleared; the cleared workspace gives
+    finite gradients bit-identical to the first run.  8 streams (each stream's
+    first chunk counts toward the epoch's advance) and 256 (the head-summing
+    workgroups and the last of each XCD count)."""
     g = torch.Generator().manual_seed(43)
     lam = lam_uniform(H, 0.9, 0.9999, g)
     V = torch.randn(B, H, N, 64, generator=g).to(torch.bfloat16)  # 128 or 2 backward chunks per stream
@@ -121,22 +122,24 @@ def test_backward_give_up_is_flagged_not_hung(hip_device, kdecay_lib, B, H, N):
         probe = V[:, :, :1].to(hip_device)  # selects the workspace of this device and stream
         assert kilat_amd.workspace_error(probe) == 0
         kdecay_lib.kdecay_debug_set_spin_limit(1)
-        flagged = []
+        gave_up = False
         try:
             for k in range(3):
                 print(f"  forced give-up backward {k}", flush=True)
                 dv, dl, _ = gpu_grads(lam, V, gy, hip_device)
                 torch.cuda.synchronize()
-                nan = bool(torch.isnan(dv).any()) or bool(torch.isnan(dl).any())
                 err = kilat_amd.workspace_error(probe)
-                # the launch that first sets the sticky word leaves NaN in what it could not compute
-                if err and not flagged:
-                    assert nan, f"launch {k} gave up but its gradients are all finite"
-                flagged.append(err)
+                if gave_up:  # the word was set before this pass: all of it NaN
+                    assert bool(torch.isnan(dv).all()) and bool(torch.isnan(dl).all()), k
+                elif err:  # the pass that gave up: NaN where it could not compute
+                    assert bool(torch.isnan(dv).any()) or bool(torch.isnan(dl).any()), k
+                    gave_up = True
         finally:
             kdecay_lib.kdecay_debug_set_spin_limit(0)
-        assert kilat_amd.workspace_error(probe) == 1
-        _workspaces[(hip_device.index, _stream_ptr(hip_device))][8:12].view(torch.int32).fill_(0)
+        assert gave_up and kilat_amd.workspace_error(probe) == 1
+        dv, dl, _ = gpu_grads(lam, V, gy, hip_device)
+        assert bool(torch.isnan(dv).all()) and bool(torch.isnan(dl).all())
+        assert kilat_amd.workspace_error(probe, clear=True) == 1  # reads the word, then zeroes the workspace
         dv1, dl1, _ = gpu_grads(lam, V, gy, hip_device)
         assert kilat_amd.workspace_error(probe) == 0
     assert torch.equal(dv1, dv0) and torch.equal(dl1, dl0)

@@ -16,7 +16,8 @@ import kilat_amd
 from kilat_amd import _lib
 from oracle import c_oracle as C
 from oracle import decay_oracle as O
-from tests.decay_cases import c1_inputs, c2_inputs, c4_inputs, elementwise_rel, lam_uniform, max_abs, rel_err
+from tests.decay_cases import (assert_rounded_once, c1_inputs, c2_inputs, c4_inputs, elementwise_rel, lam_uniform,
+                               max_abs, rel_err)
 
 pytestmark = pytest.mark.gpu
 
@@ -202,6 +203,23 @@ def test_chunk_size_switch_short_chains(hip_device, kdecay_lib, B, N, nchunk):
     assert rel_err(fin, sref) <= 1e-5
 
 
+def assert_same_rounding_as_fp32_output(lam, V, y, dev, ref32, what=""):
+    """The scan with a 2-byte output gives bit for bit its own fp32 output
+    rounded by torch (round-to-nearest-even): both are the same kernel's fp32
+    values, stored once rounded and once not.  And those fp32 values meet the
+    fp32 tolerance against the oracle's fp32 output (rel_err <= 1e-5 per
+    stream), so the 2-byte output is one rounding of values that match the
+    reference's."""
+    y32 = kilat_amd.global_decay_scan(lam.to(dev), V.to(dev), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert y32.dtype == torch.float32
+    same = torch.equal(y.to(dev), y32.to(y.dtype))
+    e = rel_err(y32, ref32)
+    print(f"  {what}: 2-byte output == fp32 output rounded: {same}; fp32 output rel_err {e:.2e}", flush=True)
+    assert same, what
+    assert e <= 1e-5, f"{what}: fp32 output rel_err {e:.3e}"
+
+
 def test_c1_fp32_full(hip_device, kdecay_lib):
     """C1 to the fp32 tolerance, read normwise per stream (max|y-ref| / max|ref|
     <= 1e-5, the gate).  The elementwise ratio |y-ref|/|ref| over elements
@@ -223,35 +241,63 @@ def test_c1_fp32_full(hip_device, kdecay_lib):
 
 
 def test_c2_bf16_full(hip_device, kdecay_lib):
+    """C2 to the bf16 tolerance, and its output rounding pinned: one
+    round-to-nearest-even from fp32, against the oracle and against the
+    kernel's own fp32 output."""
     lam, V = c2_inputs()
     y, fin = gpu_scan(lam, V, hip_device, return_final_state=True)
-    ref, sref = O.scan(lam, V)
+    ref32, sref = O.scan(lam, V, out_dtype=torch.float32)
+    ref = ref32.to(torch.bfloat16)  # the oracle's bf16 output: the same rows rounded once
     assert_parity(y, ref, torch.bfloat16, "C2")
     assert rel_err(fin, sref) <= 1e-5
     assert kilat_amd.workspace_error(V.to(hip_device)) == 0
+    assert_rounded_once(y, ref32, "C2 bf16")
+    assert_same_rounding_as_fp32_output(lam, V, y, hip_device, ref32, "C2 bf16")
 
 
-def test_c4_fp32_output_long_context(hip_device, kdecay_lib):
+def test_fp16_output_rounding_c2_shape(hip_device, kdecay_lib):
+    """fp16 V at the C2 shape: the same two rounding checks as C2's bf16."""
+    lam, V = c2_inputs(seed=12)
+    V = V.float().to(torch.float16)
+    y = gpu_scan(lam, V, hip_device)
+    ref32, _ = O.scan(lam, V, out_dtype=torch.float32)
+    assert y.dtype == torch.float16
+    assert_parity(y, ref32.to(torch.float16), torch.float16, "C2 shape fp16")
+    assert_rounded_once(y, ref32, "C2 shape fp16")
+    assert_same_rounding_as_fp32_output(lam, V, y, hip_device, ref32, "C2 shape fp16")
+
+
+@pytest.fixture(scope="module")
+def c4_oracle():
+    """C4's inputs and the oracle's fp32 output and final state (65,536 steps
+    on the CPU), shared by the C4 tests."""
+    lam, V = c4_inputs()
+    ref32, sref = O.scan(lam, V, out_dtype=torch.float32)
+    return lam, V, ref32, sref
+
+
+def test_c4_fp32_output_long_context(hip_device, kdecay_lib, c4_oracle):
     """C4 (D=128: two channel groups per head; 4096 chunks, several rounds)
     with an fp32 output, against the oracle's fp32 output at the fp32
     tolerance: late rows of the lam ~ 0.99999 heads are small, and only a
     tight relative check sees their carries."""
-    lam, V = c4_inputs()
+    lam, V, ref, sref = c4_oracle
     y, fin = gpu_scan(lam, V, hip_device, return_final_state=True, out_dtype=torch.float32)
-    ref, sref = O.scan(lam, V, out_dtype=torch.float32)
     assert y.dtype == torch.float32
     assert_parity(y, ref, torch.float32, "C4 fp32 out")
     assert rel_err(fin, sref) <= 1e-5
 
 
-def test_c4_bf16_long_context(hip_device, kdecay_lib):
-    lam, V = c4_inputs()
+def test_c4_bf16_long_context(hip_device, kdecay_lib, c4_oracle):
+    lam, V, ref32, sref = c4_oracle
     y, fin = gpu_scan(lam, V, hip_device, return_final_state=True)
-    ref, sref = O.scan(lam, V)
+    ref = ref32.to(torch.bfloat16)  # the oracle's bf16 output: the same rows rounded once
     assert_parity(y, ref, torch.bfloat16, "C4")
     assert rel_err(fin, sref) <= 1e-5
     # the carry crosses 512 chunks per stream: the last rows depend on all of them
     assert max_abs(y[:, :, -4096:], ref[:, :, -4096:]) <= 2e-2
+    assert_rounded_once(y, ref32, "C4 bf16")
+    assert_same_rounding_as_fp32_output(lam, V, y, hip_device, ref32, "C4 bf16")
 
 
 def test_sequential_kernel_matches_oracle_bits(hip_device, kdecay_lib):
@@ -417,13 +463,15 @@ def test_workspace_clean_after_suite(hip_device, kdecay_lib):
 
 
 def test_lookback_give_up_is_flagged_not_hung(hip_device, kdecay_lib):
-    """Force the bounded look-back waits to give up after two polls
+    """Force the bounded look-back waits to give up after one poll
     (kdecay_debug_set_spin_limit, the library's test hook): every launch still
-    returns and sets the workspace's sticky error word, the launch that gives
-    up writes NaN in the rows whose carry it could not compute, and once the hook and the word are cleared the same workspace
-    serves a normal launch bit-identical to the first."""
-    from kilat_amd.triton_ops import _stream_ptr, _workspaces
-
+    returns and sets the workspace's sticky error word, and the launch that
+    gives up writes NaN in the rows whose carry it could not compute.  From
+    then on the workspace is poisoned: every later launch on it, with the
+    normal poll limit again, writes NaN to every row and to the final state
+    (never finite values read from words the launch that gave up left
+    behind), until the workspace is cleared; the cleared workspace serves a
+    launch bit-identical to the first."""
     g = torch.Generator().manual_seed(41)
     lam = lam_uniform(16, 0.99, 0.99999, g).to(hip_device)
     V = torch.randn(1, 16, 32768, 128, generator=g).to(torch.bfloat16).to(hip_device)  # 64 chunks per stream
@@ -434,22 +482,30 @@ def test_lookback_give_up_is_flagged_not_hung(hip_device, kdecay_lib):
         torch.cuda.synchronize()
         assert kilat_amd.workspace_error(V) == 0
         kdecay_lib.kdecay_debug_set_spin_limit(1)
-        flagged = False
+        gave_up = False
         try:
             for k in range(3):
                 print(f"  forced give-up launch {k}", flush=True)
                 y, fin = kilat_amd.global_decay_scan(lam, V, return_final_state=True)
                 torch.cuda.synchronize()
                 err = kilat_amd.workspace_error(V)
-                if err and not flagged:  # the launch that gave up: NaN, not finite wrong values
+                if gave_up:  # the word was set before this launch: all of it NaN
+                    assert bool(torch.isnan(y).all()) and bool(torch.isnan(fin).all()), k
+                elif err:  # the launch that gave up: NaN, not finite wrong values
                     assert bool(torch.isnan(y).any()), k
-                    flagged = True
-                if not err:
+                    gave_up = True
+                else:
                     assert bool(torch.isfinite(y).all()), k
         finally:
             kdecay_lib.kdecay_debug_set_spin_limit(0)
+        assert gave_up and kilat_amd.workspace_error(V) == 1
+        print("  launch on the poisoned workspace", flush=True)
+        y, fin = kilat_amd.global_decay_scan(lam, V, return_final_state=True)
+        torch.cuda.synchronize()
+        assert bool(torch.isnan(y).all()) and bool(torch.isnan(fin).all())
         assert kilat_amd.workspace_error(V) == 1
-        _workspaces[(hip_device.index, _stream_ptr(hip_device))][8:12].view(torch.int32).fill_(0)
+        assert kilat_amd.workspace_error(V, clear=True) == 1  # reads the word, then zeroes the workspace
+        print("  launch on the cleared workspace", flush=True)
         y = kilat_amd.global_decay_scan(lam, V)
         torch.cuda.synchronize()
         assert kilat_amd.workspace_error(V) == 0

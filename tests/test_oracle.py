@@ -18,7 +18,7 @@ import torch
 
 from oracle import c_oracle as C
 from oracle import decay_oracle as O
-from tests.decay_cases import c1_inputs, lam_uniform, rel_err
+from tests.decay_cases import assert_rounded_once, c1_inputs, c2_inputs, lam_uniform, ordered_bits, rel_err
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "decay_golden.npz")
 
@@ -346,3 +346,37 @@ def test_e2e_model_runs_on_cpu_with_oracle_decay():
     with torch.no_grad():
         logits, loss = model(ids, labels=ids)
     assert logits.shape == (2, 9, 128) and torch.isfinite(loss)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rounding_check_catches_truncation_and_double_rounding(dtype):
+    """The check the GPU tests apply to 2-byte outputs (assert_rounded_once):
+    the oracle's 2-byte output is its fp32 output rounded once to nearest-even
+    (what out = zeros_like(V) does, triton_ops.py:240,246); the check accepts
+    it, and values one ulp off on a few elements; it rejects a truncating
+    store (about half the elements off) and a double rounding through a
+    narrower mantissa."""
+    lam, V = c2_inputs(seed=7, B=2, N=600, H=4)
+    V = V.float().to(dtype)
+    y2, _ = O.scan(lam, V)
+    y32, _ = O.scan(lam, V, out_dtype=torch.float32)
+    assert torch.equal(y2, y32.to(dtype))  # one rounding, nearest-even
+    assert_rounded_once(y2, y32, "oracle")
+    # one ulp off on 1 element in 2000: still accepted
+    flat = ordered_bits(y2).reshape(-1).clone()
+    flat[::2000] += 1
+    near = torch.where(flat < 0, (-flat) | 0x8000, flat).to(torch.int16).view(dtype).reshape(y2.shape)
+    assert_rounded_once(near, y32, "one ulp off on a few elements")
+    # a truncating store: the fp32 value cut towards zero to the type's significand
+    sig = 8 if dtype == torch.bfloat16 else 11
+    m, e = torch.frexp(y32.double())
+    trunc = (torch.trunc(m * 2 ** sig) / 2 ** sig * torch.pow(2.0, e.double())).to(dtype)
+    d = (ordered_bits(trunc) - ordered_bits(y2)).abs()
+    assert 0.3 <= float((d != 0).double().mean()) <= 0.7
+    with pytest.raises(AssertionError):
+        assert_rounded_once(trunc, y32, "truncated")
+    # rounding twice: first to a significand 3 bits shorter, then to the type
+    coarse = (torch.round(m * 2 ** (sig - 3)) / 2 ** (sig - 3) * torch.pow(2.0, e.double())).float()
+    with pytest.raises(AssertionError):
+        assert_rounded_once(coarse.to(dtype), y32, "rounded twice")
+

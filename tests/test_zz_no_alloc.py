@@ -105,3 +105,22 @@ def test_noalloc_replays_from_a_graph(hip_device, kdecay_lib):
         torch.cuda.synchronize()
         assert torch.equal(y, y_ref) and torch.equal(fin, f_ref), r
         assert torch.equal(w, w_ref), r
+
+
+def test_noalloc_first_call_of_a_process_under_capture(hip_device, kdecay_lib):
+    """The first no-alloc call of a process made under stream capture: the
+    library records no set-up work into the graph (the device array is
+    zero-filled by the code object loader, and the library never clears it),
+    so the captured scan alone runs on every replay.  Run in a fresh child
+    process (a subprocess, so this process's earlier calls do not count)."""
+    import os
+    import subprocess
+    import sys
+
+    script = os.path.join(os.path.dirname(os.path.abspath(__file__)), "noalloc_first_capture.py")
+    print("  child process: first noalloc call under capture", flush=True)
+    proc = subprocess.run([sys.executable, "-u", script], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
+                          timeout=100)
+    print(proc.stdout[-2000:], flush=True)
+    assert proc.returncode == 0, f"child exited {proc.returncode}"
+    assert "noalloc-first-capture ok" in proc.stdout
