@@ -42,6 +42,8 @@
 
 namespace kd {
 
+constexpr int ilog2(int n) { return n <= 1 ? 0 : 1 + ilog2(n / 2); }
+
 // --------------------------------------------------------------------------
 // Element conversion
 // --------------------------------------------------------------------------
@@ -193,31 +195,29 @@ __device__ __forceinline__ float z_of(float lam, int64_t t) {
 // cases are selects instead of branches.  The scan kernels keep the
 // loop: they build their z tables while their rows are in flight, and there
 // the shorter form measured 3.7% slower (bf16, B=8 N=4096 H=12 D=64).
-__device__ __forceinline__ float pow_like_torch_fast(float x, int64_t e) {
-  double r;
-  if (e >= 0 && e < (1 << 12)) {
-    const unsigned u = (unsigned)e;
-    double xd = (double)x;
-    r = 1.0;
+// x^e by binary exponentiation for 0 <= e < 2^BITS, unrolled and branch-free
+// (the products of ipow_f64, in the same order).
+template <int BITS>
+__device__ __forceinline__ double ipow_f64_bits(double x, unsigned e) {
+  double r = 1.0;
 #pragma unroll
-    for (int k = 0; k < 12; ++k) {
-      const double rx = r * xd;
-      r = (u >> k) & 1u ? rx : r;
-      xd *= xd;
-    }
-  } else if (e >= 0 && e < (1 << 16)) {
-    const unsigned u = (unsigned)e;
-    double xd = (double)x;
-    r = 1.0;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const double rx = r * xd;
-      r = (u >> k) & 1u ? rx : r;
-      xd *= xd;
-    }
-  } else {
-    r = ipow_f64((double)x, e);
+  for (int k = 0; k < BITS; ++k) {
+    const double rx = r * x;
+    r = (e >> k) & 1u ? rx : r;
+    x *= x;
   }
+  return r;
+}
+
+// ipow_f64 with the unrolled form for exponents below 2^16.
+__device__ __forceinline__ double ipow_f64_fast(double x, int64_t e) {
+  if (e >= 0 && e < (1 << 12)) return ipow_f64_bits<12>(x, (unsigned)e);
+  if (e >= 0 && e < (1 << 16)) return ipow_f64_bits<16>(x, (unsigned)e);
+  return ipow_f64(x, e);
+}
+
+__device__ __forceinline__ float pow_like_torch_fast(float x, int64_t e) {
+  const double r = ipow_f64_fast((double)x, e);
   const float p2 = x * x;
   const float p3 = p2 * x;
   return e == 1 ? x : e == 2 ? p2 : e == 3 ? p3 : e == 0 ? 1.0f : (float)r;
@@ -958,13 +958,22 @@ struct BwdArgs {
 // each XCD dispatches its share in index order.
 constexpr int kXcds = 8;
 
-// d(1/z)/dlam for z = (1 - lam^e) / ((1 - lam) + 1e-6), evaluated in double.
-__device__ __forceinline__ float dinvz_dlam(float lam, int64_t e) {
+// The backward's terms of one row with exponent e = t + 1, from one power:
+//   x = 1/z = ((1 - lam) + 1e-6) / (1 - lam^e)   (lam^e as z_of takes it)
+//   y = d(1/z)/dlam = (e lam^(e-1) ((1 - lam) + 1e-6) - (1 - lam^e)) / (1 - lam^e)^2
+// lam^(e-1) is evaluated in double and lam^e is its product with lam; y's numerator, a small difference of nearly equal terms
+// when lam is close to 1, stays in double, and both quotients are fp32
+// divisions.  (Two double-precision power loops and a double division per
+// row were most of the table's cost; it is built by every workgroup for its
+// chunk's rows, on the critical path after the rows arrive.)
+__device__ __forceinline__ void bwd_row_terms(float lam, int64_t e, float& x, float& y) {
   const double l = lam;
   const double p = ipow_f64(l, e - 1);
-  const double A = 1.0 - p * l;
-  const double Bd = (1.0 - l) + 1e-6;
-  return (float)(((double)e * p * Bd - A) / (A * A));
+  const double pe = p * l;
+  const float pf = e == 1 ? lam : e == 2 ? lam * lam : e == 3 ? (lam * lam) * lam : (float)pe;
+  x = ((1.0f - lam) + 1e-6f) / (1.0f - pf);
+  const double A = 1.0 - pe;
+  y = (float)((double)e * p * ((1.0 - l) + 1e-6) - A) / (float)(A * A);
 }
 
 // Value of `x` held K row groups above (row groups S lanes apart; lanes with
@@ -1005,14 +1014,20 @@ struct ChunkBwd {
 
   // Per row of the chunk (i = the row's index in its lane, 0 <= i < R):
   // x = 1/z, y = d(1/z)/dlam, z = x (i+1) lam^i + y lam^(i+1), w = x lam^i
-  // (zero for rows past the end).
+  // (zero for rows past the end).  Entry of row r: rt4[r + r / R], one entry
+  // of padding after each lane's R rows: the GW row groups of a wavefront
+  // read their own rows' entries at once, R entries (R * 16 bytes) apart,
+  // which without the padding all fell into the same LDS banks (an 8-way
+  // conflict on every table read of the sweeps).  kq likewise has a padded
+  // row: its 64 lanes' writes hit 16-way conflicts with rows of DG floats.
+  static constexpr int TS = R + 1;  // table entries per row group
   struct Smem {
-    float4 rt4[L];
+    float4 rt4[G * TS];
     float pw[G + 1];   // lam^(R*k)
     float pl[R + 1];   // lam^i
     float wt[NW][DG];  // forward per-wavefront totals
     float rt[NW][DG];  // reverse per-wavefront totals
-    float kq[G][DG];   // the carry coefficient K of every lane
+    float kq[G][DG + 1];  // the carry coefficient K of every lane
     float carry_s[DG]; // state before the chunk's first row
     float carry_g[DG]; // g after the chunk's last row
     float gfin[DG];    // final-state gradient (last chunk only; zero elsewhere)
@@ -1042,11 +1057,11 @@ struct ChunkBwd {
       }
     }
     dq = 0.0f;
-    float2 tz = *reinterpret_cast<const float2*>(&sm.rt4[g * R]);
-    float2 tc = GY ? *reinterpret_cast<const float2*>(&sm.rt4[g * R].z) : make_float2(0.0f, 0.0f);
+    float2 tz = *reinterpret_cast<const float2*>(&sm.rt4[g * TS]);
+    float2 tc = GY ? *reinterpret_cast<const float2*>(&sm.rt4[g * TS].z) : make_float2(0.0f, 0.0f);
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      const int in = g * R + (i + 1 < R ? i + 1 : i);
+      const int in = g * TS + (i + 1 < R ? i + 1 : i);
       const float2 tn = *reinterpret_cast<const float2*>(&sm.rt4[in]);
       const float2 cn = GY ? *reinterpret_cast<const float2*>(&sm.rt4[in].z) : tc;
       float v[VW], gv[VW];
@@ -1105,10 +1120,10 @@ struct ChunkBwd {
       qz[j] = 0.0f;
       ra[j] = 0.0f;
     }
-    float2 tc = *reinterpret_cast<const float2*>(&sm.rt4[g * R].z);
+    float2 tc = *reinterpret_cast<const float2*>(&sm.rt4[g * TS].z);
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      const float2 tn = *reinterpret_cast<const float2*>(&sm.rt4[g * R + (i + 1 < R ? i + 1 : i)].z);
+      const float2 tn = *reinterpret_cast<const float2*>(&sm.rt4[g * TS + (i + 1 < R ? i + 1 : i)].z);
       float gv[VW];
       opaque(rg[i]);
       unpack16<T>(rg[i], gv);
@@ -1142,7 +1157,7 @@ struct ChunkBwd {
           float gv[VW];
           opaque(rg[i]);
           unpack16<T>(rg[i], gv);
-          const float rz = sm.rt4[g * R + i].x;
+          const float rz = sm.rt4[g * TS + i].x;
 #pragma unroll
           for (int j = 0; j < VW; ++j) gn[j] = __builtin_fmaf(lam, gn[j], gv[j] * rz);
           store_vec<T, VW>(dp + (int64_t)i * a.dn, gn);
@@ -1159,7 +1174,7 @@ struct ChunkBwd {
       float gv[VW];
       opaque(rg[i]);
       unpack16<T>(rg[i], gv);
-      const float rz = sm.rt4[g * R + i].x;
+      const float rz = sm.rt4[g * TS + i].x;
 #pragma unroll
       for (int j = 0; j < VW; ++j) gn[j] = __builtin_fmaf(lam, gn[j], gv[j] * rz);
       if (i == fin_i) {
@@ -1236,14 +1251,14 @@ struct ChunkBwd {
     if (tid <= G) sm.pw[tid] = pow_like_torch(lam, (int64_t)tid * R);
     if (tid >= NT - (R + 1)) sm.pl[tid - (NT - (R + 1))] = pow_like_torch(lam, (int64_t)(tid - (NT - (R + 1))));
     for (int r = tid; r < L; r += NT) {
-      const bool in = row0 + r < a.N;
       const int64_t t = a.t_offset + row0 + r;
       const int i = r % R;
-      const float x = in ? 1.0f / z_of(lam, t) : 0.0f;
-      const float y = in ? dinvz_dlam(lam, t + 1) : 0.0f;
-      const float p = pow_like_torch(lam, i), p1 = p * lam;
+      float x = 0.0f, y = 0.0f;
+      if (row0 + r < a.N) bwd_row_terms(lam, t + 1, x, y);
+      const float p = pow_like_torch(lam, i);
+      const float p1 = p * lam;
       const float w = x * p;
-      sm.rt4[r] = make_float4(x, y, __builtin_fmaf(w, (float)(i + 1), y * p1), w);
+      sm.rt4[r + r / R] = make_float4(x, y, __builtin_fmaf(w, (float)(i + 1), y * p1), w);
     }
     if (tid < DG) {
       sm.carry_s[tid] = cs;
