@@ -280,8 +280,9 @@ def measured_traffic():
 def bench_forward_dtypes(torch, dev, steps=100):
     """The C2 shape (B=8 N=4096 H=12) with other I/O types than the headline's
     bf16: fp16, fp32 in and out (D=64: two 128-byte channel groups per head, so
-    twice the bytes and 1.5 rounds; D=32: C2's bytes), and bf16 in / fp32 out.
-    Algorithmic bytes: V read once, y written once.  4 rotated sets."""
+    twice the bytes; D=32: C2's bytes), bf16 in / fp32 out, and bf16 with
+    D=128 (twice the bytes).  Algorithmic bytes: V read once, y written once.
+    4 rotated sets."""
     from kilat_amd import _lib
     from kilat_amd.triton_ops import _stream_ptr, _workspace
 
@@ -292,8 +293,9 @@ def bench_forward_dtypes(torch, dev, steps=100):
     stream = _stream_ptr(dev)
     out = {}
     for name, ti, to, D in (("f16", torch.float16, torch.float16, 64), ("f32_d64", torch.float32, torch.float32, 64),
-                            ("f32_d32", torch.float32, torch.float32, 32), ("bf16_in_f32_out", torch.bfloat16,
-                                                                             torch.float32, 64)):
+                            ("f32_d32", torch.float32, torch.float32, 32),
+                            ("bf16_in_f32_out", torch.bfloat16, torch.float32, 64),
+                            ("bf16_d128", torch.bfloat16, torch.bfloat16, 128)):
         g = torch.Generator(device=dev).manual_seed(11)
         sets = [(torch.randn(B, H, N, D, generator=g, device=dev).to(ti), torch.empty(B, H, N, D, device=dev, dtype=to))
                 for _ in range(4)]
@@ -338,11 +340,16 @@ def bench_backward(torch, dev, steps=100):
     ws = _workspace(dev, stream, nbytes)
     sets = []
     nset = 4
-    for _ in range(nset):
-        V = torch.randn(B, H, N, D, generator=g, device=dev).to(torch.bfloat16)
-        gy = torch.randn(B, H, N, D, generator=g, device=dev).to(torch.bfloat16)
-        sets.append((V, gy, torch.empty_like(V), torch.empty_like(V), torch.empty(nst, device=dev),
-                     torch.empty(H, device=dev), torch.empty(B, H, D, device=dev)))
+    # V, gy, y and dV of every set carved from one allocation, as the headline's
+    # sets are (separate caching-allocator blocks measured slower).
+    n = B * H * N * D
+    buf = torch.empty(4 * nset * n, dtype=torch.bfloat16, device=dev)
+    for k in range(nset):
+        V, gy, y, dV = (buf[(4 * k + j) * n:(4 * k + j + 1) * n].view(B, H, N, D) for j in range(4))
+        V.copy_(torch.randn(B, H, N, D, generator=g, device=dev))
+        gy.copy_(torch.randn(B, H, N, D, generator=g, device=dev))
+        sets.append((V, gy, y, dV, torch.empty(nst, device=dev), torch.empty(H, device=dev),
+                     torch.empty(B, H, D, device=dev)))
     st = _lib.strides4(sets[0][0].stride())
     rc = [0]
 
@@ -362,7 +369,6 @@ def bench_backward(torch, dev, steps=100):
     rb, _ = time_region(torch, bwd, steps, 100, events=False)
     if rc[0]:
         raise RuntimeError("training scan failed: " + lib.kdecay_last_error_string().decode())
-    n = B * H * N * D
     fus, bus = rf * 1e3 / steps, rb * 1e3 / steps
     return {"config": "C2 shape, bf16: forward with saved states, then backward (dV, dlam)",
             "fwd_train_us": round(fus, 3), "fwd_train_GBps": round(4 * n / (fus * 1e-6) / 1e9, 1),

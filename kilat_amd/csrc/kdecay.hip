@@ -1717,9 +1717,11 @@ int64_t group_width(int v_dtype, int64_t D) {
   return D < full ? D : full;
 }
 
-// Chunk shape: R rows per lane, NW wavefronts per workgroup.
+// Chunk shape: R rows per lane, NW wavefronts per workgroup; `six`: the
+// 8-row grid built for six workgroups per compute unit (see chunk_shape).
 struct ChunkShape {
   int R, NW;
+  bool six = false;
 };
 
 int64_t chunk_rows(int v_dtype, int64_t D, ChunkShape c) {
@@ -1751,12 +1753,48 @@ constexpr int64_t kSmallGrid = 416;
 constexpr int64_t kSmallGrid2 = 640;
 constexpr int64_t kSmallGrid1 = 160;
 
+// Grids of 16-row chunks just above one resident round.  The 16-row kernels
+// take 104-110 VGPRs, four workgroups per compute unit, 1024 on the 256 CUs
+// of a gfx950 part; above that the launch runs a second, partial round, and
+// at 1.5 rounds it lost 8-10 points of bandwidth against C2 and C4.  Held
+// in 80 VGPRs (every 80-VGPR build of the 16-row kernel spilled 104-292
+// bytes) the 8-row kernel runs six workgroups per compute unit, 1536 at
+// once, so the same launch takes at most two full rounds of 256-row chunks,
+// with a look-back window of 1 (the second round's chunks find their
+// predecessors' inclusive words published in the first).  Measured (same-box
+// A/B, us, 16-row kernel / 8-row six-per-CU window 1, all N=4096 H=12):
+// bf16 D=128 B=6 (1152 chunks at 16 rows) 29.78 / 28.23, B=7 (1344) 35.19 /
+// 31.67, B=8 (1536) 40.84 / 35.75 (61.6% -> 70.4% of 8 TB/s); fp32 D=64
+// B=6 29.55 / 27.87, B=7 34.26 / 31.36, B=8 39.93 / 35.39 (63.0% -> 71.1%);
+// bf16 D=64 B=11 (1056) 28.31 / 27.22, B=12 (1152) 28.94 / 29.45, B=13
+// (1248) 31.01 / 31.72, B=14 (1344) 35.62 / 33.03, B=15 (1440) 37.45 /
+// 35.41, B=16 (1536) 39.67 / 38.14.  Windows 2 and 4 were slower (bf16
+// D=128 B=8: 37.7 and 37.4 us), and so was the 8-row grid outside this
+// range: C2 (768, one round) 17.56 / 22.9 (window 2: 18.9), B=16 H=16 D=64
+// (2048) 46.68 / 49.26, B=24 (2304) 57.8 / 60.1, C4 (4096) 91.5 / 169
+// (window 4: 91.2), longer chains (16 chunks per stream: B=8 N=8192 H=12
+// D=64 34.87 / 41.32, window 2 35.67).  So: 8 or fewer chunks per stream
+// and 1280 < chunks <= 1536, or 1024 < chunks <= 1536 when a head has
+// several channel groups (its streams then read strided halves of each row,
+// where the 16-row kernel does worse).  Full 128-byte channel groups only:
+// the 8-row kernel of narrower groups (more row groups per wavefront, a
+// longer scan across them) spilled 36-60 bytes within 80 VGPRs.
+constexpr int64_t kSixLo = 1280;
+constexpr int64_t kSixLoGroups = 1024;
+constexpr int64_t kSixHi = 1536;
+constexpr int64_t kSixChain = 8;
+
 ChunkShape chunk_shape(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   const int64_t L = chunk_rows(v_dtype, D, ChunkShape{kR, kNW});
-  const int64_t nstream = B * H * (D / group_width(v_dtype, D));
+  const int64_t ng = D / group_width(v_dtype, D);
+  const int64_t nstream = B * H * ng;
   const int64_t chain = (N + L - 1) / L;
+  const int64_t grid = chain * nstream;
   const int64_t lim = chain == 1 ? kSmallGrid1 : chain == 2 ? kSmallGrid2 : kSmallGrid;
-  if (chain * nstream <= lim) return ChunkShape{kRSmall, kNWSmall};
+  if (grid <= lim) return ChunkShape{kRSmall, kNWSmall};
+  const bool full = group_width(v_dtype, D) * elem_size(v_dtype) == 128;
+  if (full && chain <= kSixChain && grid > (ng > 1 ? kSixLoGroups : kSixLo) && grid <= kSixHi)
+    return ChunkShape{kRSmall, kNWSmall, true};
   return ChunkShape{kR, kNW};
 }
 
@@ -1770,7 +1808,7 @@ bool head_dim_ok(int v_dtype, int64_t D) {
 }
 
 template <typename TI, typename TO, int DG, int R = kR, int NW = kNW, int WPE = kWPE>
-int launch_chunked(const ScanArgs& a, int64_t grid, hipStream_t s) {
+int launch_chunked(const ScanArgs& a, int64_t grid, hipStream_t s, bool six = false) {
   constexpr int VW = 16 / (int)sizeof(TI);
   constexpr int LPR = DG / VW;
   // Small grids are latency-bound: there the per-row normaliser table uses
@@ -1779,6 +1817,13 @@ int launch_chunked(const ScanArgs& a, int64_t grid, hipStream_t s) {
   // 18.36 vs 18.74 us with the unrolled one).  Same values either way.
   constexpr bool FZ = R == kRSmall && NW == kNWSmall;
   if constexpr (FZ) {
+    if constexpr (LPR == 8) {  // full 128-byte channel groups
+      if (six) {  // chunk_shape's 8-row grid of at most two rounds, six workgroups per CU
+        hipLaunchKernelGGL((scan_chunked<TI, TO, LPR, R, NW, 1, 6, FZ, false>), dim3((unsigned)grid), dim3(NW * 64), 0,
+                           s, a);
+        return hip_check("scan_chunked launch");
+      }
+    }
     // Small grids run in one round.  Long chains of few streams want a wide
     // window: a chunk then folds the aggregates of its predecessors, each
     // published as soon as that chunk is scanned, instead of waiting for their
@@ -1830,12 +1875,12 @@ int launch_chunked(const ScanArgs& a, int64_t grid, hipStream_t s) {
 
 // DG: channels per stream (group_width); R, NW: the chunk shape (chunk_shape).
 template <typename TI, typename TO, int R, int NW>
-int dispatch_dg_r(const ScanArgs& a, int64_t DG, int64_t grid, hipStream_t s) {
+int dispatch_dg_r(const ScanArgs& a, int64_t DG, int64_t grid, hipStream_t s, bool six) {
   switch (DG) {
-    case 16: return launch_chunked<TI, TO, 16, R, NW>(a, grid, s);
-    case 32: return launch_chunked<TI, TO, 32, R, NW>(a, grid, s);
+    case 16: return launch_chunked<TI, TO, 16, R, NW>(a, grid, s, six);
+    case 32: return launch_chunked<TI, TO, 32, R, NW>(a, grid, s, six);
     case 64:
-      if constexpr (sizeof(TI) == 2) return launch_chunked<TI, TO, 64, R, NW>(a, grid, s);
+      if constexpr (sizeof(TI) == 2) return launch_chunked<TI, TO, 64, R, NW>(a, grid, s, six);
       break;
   }
   return fail(KDECAY_ESHAPE, "unsupported channel group %lld", (long long)DG);
@@ -1843,8 +1888,8 @@ int dispatch_dg_r(const ScanArgs& a, int64_t DG, int64_t grid, hipStream_t s) {
 
 template <typename TI, typename TO>
 int dispatch_dg(const ScanArgs& a, int64_t DG, int64_t grid, hipStream_t s, ChunkShape c) {
-  if (c.R == kRSmall && c.NW == kNWSmall) return dispatch_dg_r<TI, TO, kRSmall, kNWSmall>(a, DG, grid, s);
-  return dispatch_dg_r<TI, TO, kR, kNW>(a, DG, grid, s);
+  if (c.R == kRSmall && c.NW == kNWSmall) return dispatch_dg_r<TI, TO, kRSmall, kNWSmall>(a, DG, grid, s, c.six);
+  return dispatch_dg_r<TI, TO, kR, kNW>(a, DG, grid, s, false);
 }
 
 // Launch shape of the backward scan: 4 wavefronts; 16 rows per lane (512-row

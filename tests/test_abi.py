@@ -68,6 +68,17 @@ def test_workspace_bytes(kdecay_lib):
     assert ws(10, 16, 512, 64, _lib.KDECAY_BF16) == 256 + 10 * 16 * 2 * 64 * 8  # 160, 1 per stream: 8 rows
     assert ws(11, 16, 512, 64, _lib.KDECAY_BF16) == 0  # 176 single-chunk streams: 16 rows, no look-back
     assert ws(2, 6, 1024, 48, _lib.KDECAY_BF16) == 0  # unsupported D
+    # Just above one resident round of 512-row chunks (8 or fewer per stream, full
+    # 128-byte groups): 256-row chunks, six workgroups per compute unit.
+    assert ws(13, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + 13 * 12 * 8 * 64 * 8  # 1248: 16 rows
+    assert ws(14, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + 14 * 12 * 16 * 64 * 8  # 1344: 8 rows
+    assert ws(16, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + 16 * 12 * 16 * 64 * 8  # 1536: 8 rows
+    assert ws(17, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + 17 * 12 * 8 * 64 * 8  # 1632: 16 rows
+    assert ws(14, 12, 4097, 64, _lib.KDECAY_BF16) == 256 + 14 * 12 * 9 * 64 * 8  # 9 per stream: 16 rows
+    assert ws(5, 12, 4096, 128, _lib.KDECAY_BF16) == 256 + 5 * 12 * 8 * 128 * 8  # 960 in 2 groups: one round, 16 rows
+    assert ws(6, 12, 4096, 128, _lib.KDECAY_BF16) == 256 + 6 * 12 * 16 * 128 * 8  # 1152 in 2 groups: 8 rows
+    assert ws(8, 12, 4096, 64, _lib.KDECAY_F32) == 256 + 8 * 12 * 16 * 64 * 8  # 1536 in 2 groups: 8 rows
+    assert ws(32, 12, 4096, 32, _lib.KDECAY_BF16) == 256 + 32 * 12 * 4 * 32 * 8  # 1536 of 64-byte rows: 1024-row chunks
 
 
 def test_backward_workspace_bytes(kdecay_lib):

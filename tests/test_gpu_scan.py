@@ -203,6 +203,43 @@ def test_chunk_size_switch_short_chains(hip_device, kdecay_lib, B, N, nchunk):
     assert rel_err(fin, sref) <= 1e-5
 
 
+@pytest.mark.parametrize("dname,B,H,N,D,six", [
+    ("bf16", 13, 12, 4096, 64, False),  # 1248 chunks of 512 rows: 16 rows per lane, 2 rounds
+    ("bf16", 14, 12, 4096, 64, True),   # 1344: 256-row chunks, six workgroups per CU
+    ("bf16", 16, 12, 4096, 64, True),   # 1536
+    ("bf16", 17, 12, 4096, 64, False),  # 1632
+    ("bf16", 14, 12, 4097, 64, False),  # 9 chunks per stream
+    ("bf16", 28, 12, 2048, 64, True),   # 4 chunks per stream
+    ("bf16", 5, 12, 4096, 128, False),  # 960 in two channel groups per head: one round
+    ("bf16", 6, 12, 4096, 128, True),   # 1152
+    ("f32", 8, 12, 4096, 64, True),     # 1536 in two groups of 32 fp32 channels
+    ("f16", 16, 12, 4096, 64, True),
+])
+def test_chunk_shape_just_above_one_round(hip_device, kdecay_lib, dname, B, H, N, D, six):
+    """The switch to 256-row chunks at six workgroups per compute unit for
+    16-row grids just above one resident round (more than 1280 chunks, or 1024
+    with several channel groups per head, up to 1536, 8 or fewer per stream),
+    both sides of each bound, against the oracle; with a carried state, an
+    offset and the final state, and for bf16 also the fp32 output."""
+    dt = DTYPES[dname]
+    es = torch.empty((), dtype=dt).element_size()
+    rows = chunk_rows(dt, D, 8 if six else 16)
+    ws = kdecay_lib.kdecay_scan_workspace_bytes(B, H, N, D, {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[dt])
+    assert ws == 256 + B * H * -(-N // rows) * D * 8, (ws, rows)
+    g = torch.Generator().manual_seed(180 + B + N % 7)
+    lam = lam_uniform(H, 0.5, 0.9999, g)
+    V = torch.randn(B, H, N, D, generator=g).to(dt)
+    init = torch.randn(B, H, D, generator=g)
+    y, fin = gpu_scan(lam, V, hip_device, initial_state=init.to(hip_device), return_final_state=True, t_offset=5)
+    ref32, sref = O.scan(lam, V, init_state=init, t_offset=5, out_dtype=torch.float32)
+    assert_parity(y, ref32.to(dt), dt, f"{dname} B={B} N={N} D={D}")
+    assert rel_err(fin, sref) <= 1e-5
+    if dt == torch.bfloat16 and es == 2:
+        y32 = gpu_scan(lam, V, hip_device, initial_state=init.to(hip_device), t_offset=5, out_dtype=torch.float32)
+        assert_parity(y32, ref32, torch.float32, f"{dname} fp32 out")
+        assert torch.equal(y32.to(dt), y)
+
+
 def assert_same_rounding_as_fp32_output(lam, V, y, dev, ref32, what=""):
     """The scan with a 2-byte output gives bit for bit its own fp32 output
     rounded by torch (round-to-nearest-even): both are the same kernel's fp32
