@@ -1784,6 +1784,20 @@ constexpr int64_t kSixLoGroups = 1024;
 constexpr int64_t kSixHi = 1536;
 constexpr int64_t kSixChain = 8;
 
+// Small grids of few, long streams: 512-row chunks of 8 wavefronts x 8 rows
+// instead of 256-row chunks of 4 wavefronts, which halves the chain a carry
+// crosses.  Measured (bf16 D=64, same-box A/B, us, 4 / 8 wavefronts, chain at
+// 256 rows): B=1 N=65536 H=2 (256 per stream) 20.23 / 15.00, B=1 N=32768 H=6
+// (128) 15.60 / 12.58, B=1 N=16384 H=6 (64) 10.26 / 9.74, B=1 N=16384 H=12
+// (64) 12.32 / 11.92, B=2 N=16384 H=6 (64) 12.34 / 11.95; with 32 or fewer
+// per stream the 4-wavefront chunks stay faster: B=1 N=8192 H=6 8.10 / 8.41,
+// B=1 N=8192 H=16 9.03 / 9.38, B=2 N=8192 H=12 11.03 / 11.44, B=2 N=4096
+// H=6 7.41 / 7.82.  (At the end-to-end model's layer shape, B=8 N=1024 H=6,
+// the 4 x 8 chunk also beat 2 wavefronts x 8 rows, 4 x 4, 8 x 4 and 8 x 8:
+// 6.49 against 6.61-7.43 us.)
+constexpr int kNWLong = 8;
+constexpr int64_t kLongChain = 64;
+
 ChunkShape chunk_shape(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   const int64_t L = chunk_rows(v_dtype, D, ChunkShape{kR, kNW});
   const int64_t ng = D / group_width(v_dtype, D);
@@ -1791,8 +1805,11 @@ ChunkShape chunk_shape(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) 
   const int64_t chain = (N + L - 1) / L;
   const int64_t grid = chain * nstream;
   const int64_t lim = chain == 1 ? kSmallGrid1 : chain == 2 ? kSmallGrid2 : kSmallGrid;
-  if (grid <= lim) return ChunkShape{kRSmall, kNWSmall};
   const bool full = group_width(v_dtype, D) * elem_size(v_dtype) == 128;
+  if (grid <= lim) {
+    const int64_t chain8 = (N + L / 2 - 1) / (L / 2);  // chunks per stream at 8 rows per lane
+    return full && chain8 >= kLongChain ? ChunkShape{kRSmall, kNWLong} : ChunkShape{kRSmall, kNWSmall};
+  }
   if (full && chain <= kSixChain && grid > (ng > 1 ? kSixLoGroups : kSixLo) && grid <= kSixHi)
     return ChunkShape{kRSmall, kNWSmall, true};
   return ChunkShape{kR, kNW};
@@ -1873,6 +1890,15 @@ int launch_chunked(const ScanArgs& a, int64_t grid, hipStream_t s, bool six = fa
   return hip_check("scan_chunked launch");
 }
 
+// The long-chain small grids of chunk_shape: 8 wavefronts x 8 rows, window 16.
+template <typename TI, typename TO, int DG>
+int launch_long(const ScanArgs& a, int64_t grid, hipStream_t s) {
+  constexpr int LPR = DG / (16 / (int)sizeof(TI));
+  hipLaunchKernelGGL((scan_chunked<TI, TO, LPR, kRSmall, kNWLong, 16, kWPE, true, false>), dim3((unsigned)grid),
+                     dim3(kNWLong * 64), 0, s, a);
+  return hip_check("scan_chunked launch");
+}
+
 // DG: channels per stream (group_width); R, NW: the chunk shape (chunk_shape).
 template <typename TI, typename TO, int R, int NW>
 int dispatch_dg_r(const ScanArgs& a, int64_t DG, int64_t grid, hipStream_t s, bool six) {
@@ -1888,6 +1914,15 @@ int dispatch_dg_r(const ScanArgs& a, int64_t DG, int64_t grid, hipStream_t s, bo
 
 template <typename TI, typename TO>
 int dispatch_dg(const ScanArgs& a, int64_t DG, int64_t grid, hipStream_t s, ChunkShape c) {
+  if (c.R == kRSmall && c.NW == kNWLong) {
+    // Long chains only (window 16, fewer workgroups than twice the CUs: no throttle), full groups.
+    if constexpr (sizeof(TI) == 2) {
+      if (DG == 64) return launch_long<TI, TO, 64>(a, grid, s);
+    } else {
+      if (DG == 32) return launch_long<TI, TO, 32>(a, grid, s);
+    }
+    return fail(KDECAY_ESHAPE, "unsupported channel group %lld", (long long)DG);
+  }
   if (c.R == kRSmall && c.NW == kNWSmall) return dispatch_dg_r<TI, TO, kRSmall, kNWSmall>(a, DG, grid, s, c.six);
   return dispatch_dg_r<TI, TO, kR, kNW>(a, DG, grid, s, false);
 }

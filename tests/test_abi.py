@@ -78,6 +78,12 @@ def test_workspace_bytes(kdecay_lib):
     assert ws(5, 12, 4096, 128, _lib.KDECAY_BF16) == 256 + 5 * 12 * 8 * 128 * 8  # 960 in 2 groups: one round, 16 rows
     assert ws(6, 12, 4096, 128, _lib.KDECAY_BF16) == 256 + 6 * 12 * 16 * 128 * 8  # 1152 in 2 groups: 8 rows
     assert ws(8, 12, 4096, 64, _lib.KDECAY_F32) == 256 + 8 * 12 * 16 * 64 * 8  # 1536 in 2 groups: 8 rows
+    # Small grids of long streams: from 64 chunks of 256 rows per stream on, 512-row
+    # chunks of 8 wavefronts (full 128-byte groups).
+    assert ws(1, 6, 16128, 64, _lib.KDECAY_BF16) == 256 + 6 * 63 * 64 * 8  # 63 per stream: 256 rows
+    assert ws(1, 6, 16384, 64, _lib.KDECAY_BF16) == 256 + 6 * 32 * 64 * 8  # 64: 512 rows
+    assert ws(1, 2, 16384, 64, _lib.KDECAY_F32) == 256 + 2 * 32 * 64 * 8  # two groups of 32 fp32: 512 rows
+    assert ws(1, 2, 65536, 32, _lib.KDECAY_BF16) == 256 + 2 * 128 * 32 * 8  # 64-byte rows keep 4 x 8: 512 rows
     assert ws(32, 12, 4096, 32, _lib.KDECAY_BF16) == 256 + 32 * 12 * 4 * 32 * 8  # 1536 of 64-byte rows: 1024-row chunks
 
 

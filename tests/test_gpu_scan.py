@@ -644,13 +644,15 @@ def test_scan_wide_and_padded_head_dims(hip_device, kdecay_lib, dname, D):
 
 
 @pytest.mark.parametrize("dname,H,N", [("bf16", 3, 2000), ("bf16", 2, 5000), ("bf16", 1, 40000), ("f32", 2, 9000),
-                                       ("f16", 1, 70000)])
+                                       ("f16", 1, 70000), ("bf16", 6, 16128), ("bf16", 6, 16384),
+                                       ("f32", 2, 16384), ("bf16", 2, 65535)])
 def test_small_grid_windows(hip_device, kdecay_lib, dname, H, N):
     """Small grids (at most 416 chunks of 512 rows) of few streams with long
     chains: the one-round launch takes a look-back window of 4, 8 or 16 by
-    chunks per stream (8 rows per lane: 256-row chunks for 128-byte groups).
-    Against the C restatement at full length, with a carried state and an
-    offset; the final state too."""
+    chunks per stream (8 rows per lane: 256-row chunks for 128-byte groups),
+    and from 64 such chunks per stream on (N=16384 against 16128 here) 512-row
+    chunks of 8 wavefronts.  Against the C restatement at full length, with a
+    carried state and an offset; the final state too."""
     dtype = DTYPES[dname]
     g = torch.Generator().manual_seed(280 + N)
     lam = lam_uniform(H, 0.9, 0.99999, g)
