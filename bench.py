@@ -13,7 +13,8 @@ bandwidth, the decode step (C3: 256 x 12 x 64, launch-latency bound) and the
 long-context scan (C4: B=1 N=65536 H=16 D=128 bf16).  The CPU baseline is the
 oracle's restatement of the reference's CPU path timed on the host cores.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-extras]
+                    [--workload c2|c5_layer|c4]
 """
 from __future__ import annotations
 
@@ -47,7 +48,19 @@ def parse_args():
     p.add_argument("--rotate", type=int, default=8, help="(V, y) buffer sets cycled through")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true")
+    # The headline line is C2.  The other two time the same protocol (warm-up,
+    # rotated sets, HIP-event region) on another shape, for profiling one
+    # kernel shape alone; they print no extras and no CPU baseline.
+    p.add_argument("--workload", choices=sorted(WORKLOADS), default="c2")
     return p.parse_args()
+
+
+# name -> (B, H, N, D, description); bf16 V and y.  lam as C2's (one head at 0.9999).
+WORKLOADS = {
+    "c2": (8, 12, 4096, 64, "full-sequence global-decay scan, bf16 V/y, fp32 accumulate"),
+    "c5_layer": (8, 6, 1024, 64, "one layer of the end-to-end model's decay path (C5), bf16 V/y"),
+    "c4": (1, 16, 65536, 128, "long-context scan (C4), bf16 V/y"),
+}
 
 
 def c2_lam(H: int, torch):
@@ -261,18 +274,19 @@ def bench_long(torch, kilat_amd, dev, steps=20):
             "tokens_per_s": round(B * N / (region / steps * 1e-3), 1)}
 
 
-def measured_traffic():
-    """HBM bytes per launch of the C2 scan from the committed rocprofv3 PMC summary, or None.
+def measured_traffic(workload: str = "c2"):
+    """HBM bytes per launch of the workload's scan from the committed rocprofv3 PMC summary, or None.
 
     profiles/scan_chunked_bf16_c2_counters.json holds FETCH_SIZE and WRITE_SIZE
-    (KiB per dispatch) of the scan and of a copy kernel of known size, which
-    gives the factor each counter is scaled by.
+    (KiB per dispatch) of the scan at each workload and of a copy kernel of
+    known size, which gives the factor each counter is scaled by.
     """
     path = os.path.join(ROOT, "profiles", "scan_chunked_bf16_c2_counters.json")
+    key = {"c2": "scan", "c4": "scan_c4", "c5_layer": "scan_c5_layer"}[workload]
     try:
         with open(path) as f:
             m = json.load(f)
-        return int(round(m["scan"]["fetch_kib"] * m["fetch_scale"] * 1024 + m["scan"]["write_kib"] * m["write_scale"] * 1024))
+        return int(round(m[key]["fetch_kib"] * m["fetch_scale"] * 1024 + m[key]["write_kib"] * m["write_scale"] * 1024))
     except (OSError, KeyError, ValueError):
         return None
 
@@ -578,7 +592,8 @@ def main() -> int:
     from kilat_amd import _lib
 
     dev = torch.device("cuda", 0)
-    B, H, N, D = 8, 12, 4096, 64
+    B, H, N, D, workload = WORKLOADS[args.workload]
+    headline = args.workload == "c2"
     log(f"allocating {args.rotate} x (V, y) bf16 {B}x{H}x{N}x{D}")
     sets = rotated_sets(torch, dev, (B, H, N, D), args.rotate)
     lam = c2_lam(H, torch).to(dev)
@@ -601,8 +616,10 @@ def main() -> int:
     achieved = value
     log(f"region {ms_step * 1e3:.2f} us/step")
 
+    metric = METRIC if headline else (f"decay-scan HBM GB/s (% of peak) + tokens/sec, B={B} N={N} H={H} Dh={D} bf16 "
+                                      f"({args.workload})")
     result = {
-        "metric": METRIC,
+        "metric": metric,
         "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -614,17 +631,17 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "full-sequence global-decay scan, bf16 V/y, fp32 accumulate",
+        "config": {"workload": workload,
                    "B": B, "N": N, "H": H, "D": D, "io_dtype": "bf16", "rotated_buffer_sets": args.rotate,
                    "parallelism": "single GPU"},
         "tokens_per_s": round(B * N / (ms_step * 1e-3), 1),
         "pct_of_peak": round(100 * value / HBM_PEAK_GBPS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(),
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(args.workload),
                      "kernel_us": round(ms_step * 1e3, 3), "algorithmic_bytes": nbytes},
     }
     extras = {}
-    if not args.no_extras:
+    if headline and not args.no_extras:
         log("copy bandwidth")
         extras["copy_GBps"] = round(copy_bandwidth(torch, dev), 1)
         del sets, launch
@@ -645,7 +662,7 @@ def main() -> int:
         log("end-to-end model forward (C5)")
         extras["e2e"] = bench_e2e(torch, dev)
     result["extras"] = extras
-    if not args.no_cpu_baseline:
+    if headline and not args.no_cpu_baseline:
         log("CPU baseline (oracle restatement of the reference CPU path)")
         result["cpu_baseline"] = cpu_baseline(torch, B, H, N, D)
         if not args.no_extras:
