@@ -958,17 +958,17 @@ struct BwdArgs {
 // each XCD dispatches its share in index order.
 constexpr int kXcds = 8;
 
-// The backward's terms of one row with exponent e = t + 1, from one power:
+// The backward's terms of one row with exponent e = t + 1, from p = lam^(e-1):
 //   x = 1/z = ((1 - lam) + 1e-6) / (1 - lam^e)   (lam^e as z_of takes it)
 //   y = d(1/z)/dlam = (e lam^(e-1) ((1 - lam) + 1e-6) - (1 - lam^e)) / (1 - lam^e)^2
-// lam^(e-1) is evaluated in double and lam^e is its product with lam; y's numerator, a small difference of nearly equal terms
-// when lam is close to 1, stays in double, and both quotients are fp32
-// divisions.  (Two double-precision power loops and a double division per
-// row were most of the table's cost; it is built by every workgroup for its
-// chunk's rows, on the critical path after the rows arrive.)
-__device__ __forceinline__ void bwd_row_terms(float lam, int64_t e, float& x, float& y) {
+// lam^e is p times lam (in double); y's numerator, a small difference of
+// nearly equal terms when lam is close to 1, stays in double, and both
+// quotients are fp32 divisions.  (Two double-precision power loops and a
+// double division per row were most of the table's cost; it is built by
+// every workgroup for its chunk's rows, on the critical path after the rows
+// arrive.)
+__device__ __forceinline__ void bwd_row_terms(float lam, int64_t e, double p, float& x, float& y) {
   const double l = lam;
-  const double p = ipow_f64(l, e - 1);
   const double pe = p * l;
   const float pf = e == 1 ? lam : e == 2 ? lam * lam : e == 3 ? (lam * lam) * lam : (float)pe;
   x = ((1.0f - lam) + 1e-6f) / (1.0f - pf);
@@ -1250,15 +1250,26 @@ struct ChunkBwd {
     __syncthreads();
     if (tid <= G) sm.pw[tid] = pow_like_torch(lam, (int64_t)tid * R);
     if (tid >= NT - (R + 1)) sm.pl[tid - (NT - (R + 1))] = pow_like_torch(lam, (int64_t)(tid - (NT - (R + 1))));
-    for (int r = tid; r < L; r += NT) {
-      const int64_t t = a.t_offset + row0 + r;
-      const int i = r % R;
-      float x = 0.0f, y = 0.0f;
-      if (row0 + r < a.N) bwd_row_terms(lam, t + 1, x, y);
+    {
+      // One double-precision power per thread: lam^(e-1) of its first row,
+      // times lam^NT for each later row (NT apart).  A thread's rows share
+      // their index in the lane (NT is a multiple of R), hence lam^i.
+      static_assert(NT % R == 0 && (NT & (NT - 1)) == 0, "rows of a thread");
+      const int i = tid % R;
       const float p = pow_like_torch(lam, i);
       const float p1 = p * lam;
-      const float w = x * p;
-      sm.rt4[r + r / R] = make_float4(x, y, __builtin_fmaf(w, (float)(i + 1), y * p1), w);
+      double q = ipow_f64((double)lam, a.t_offset + row0 + tid);
+      double step = lam;
+#pragma unroll
+      for (int k = 0; k < ilog2(NT); ++k) step *= step;
+      for (int r = tid; r < L; r += NT) {
+        const int64_t t = a.t_offset + row0 + r;
+        float x = 0.0f, y = 0.0f;
+        if (row0 + r < a.N) bwd_row_terms(lam, t + 1, q, x, y);
+        const float w = x * p;
+        sm.rt4[r + r / R] = make_float4(x, y, __builtin_fmaf(w, (float)(i + 1), y * p1), w);
+        q *= step;
+      }
     }
     if (tid < DG) {
       sm.carry_s[tid] = cs;
