@@ -1037,16 +1037,21 @@ struct ChunkBwd {
   // Forward sweep over V and gy together (zero state in): sl = lane-local
   // state, wl = lane-local d(state)/dlam; dq = the sum over the lane's rows
   // and channels of u wl + e sl, with u = gy / z and e = gy d(1/z)/dlam, taken
-  // per row as rz * sum_j gy wl + rzp * sum_j gy sl.  With GY (few rows per
-  // lane, registers to spare) it also takes sweep_gy's sums, saving that
-  // pass's unpacking.  One row at a time (pin): left free, the compiler ran
-  // the whole state chain first and held every row's states.  Each row's
-  // table entry is read one row ahead.  fin_i: the lane's row N-1
-  // (final-state gradient), or -1.
-  template <bool GY>
+  // per row as rz * sum_j gy wl + rzp * sum_j gy sl.  From row F0 on it also
+  // takes sweep_gy's sums (qz, ra), saving that pass's unpacking of those
+  // rows: with few rows per lane from the first row (F0 = 0), with 16 rows
+  // from row 8, once the V rows consumed so far have freed the 16 registers
+  // the sums take (from row 6 on, 4 bytes spilled and the C2 backward was
+  // 3% slower; from row 8, 1% faster than a separate pass over all 16 rows,
+  // 27.55 against 27.9 us, same-box A/B).  One row at a time (pin): left
+  // free, the compiler ran the whole state chain first and held every row's
+  // states.  Each row's table entry is read one row ahead.  fin_i: the
+  // lane's row N-1 (final-state gradient), or -1.
+  template <int F0>
   __device__ static void sweep_fwd(const uint4 (&rv)[R], uint4 (&rg)[R], float lam, int g, int fin_i, int ds,
                                    const Smem& sm, float (&sl)[VW], float (&wl)[VW], float& dq, float (&qz)[VW],
                                    float (&ra)[VW]) {
+    constexpr bool GY = F0 < R;
 #pragma unroll
     for (int j = 0; j < VW; ++j) {
       sl[j] = 0.0f;
@@ -1057,13 +1062,10 @@ struct ChunkBwd {
       }
     }
     dq = 0.0f;
-    float2 tz = *reinterpret_cast<const float2*>(&sm.rt4[g * TS]);
-    float2 tc = GY ? *reinterpret_cast<const float2*>(&sm.rt4[g * TS].z) : make_float2(0.0f, 0.0f);
+    float4 t = sm.rt4[g * TS];
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      const int in = g * TS + (i + 1 < R ? i + 1 : i);
-      const float2 tn = *reinterpret_cast<const float2*>(&sm.rt4[in]);
-      const float2 cn = GY ? *reinterpret_cast<const float2*>(&sm.rt4[in].z) : tc;
+      const float4 tn = sm.rt4[g * TS + (i + 1 < R ? i + 1 : i)];
       float v[VW], gv[VW];
       unpack16<T>(rv[i], v);
       unpack16<T>(rg[i], gv);
@@ -1074,27 +1076,26 @@ struct ChunkBwd {
         sl[j] = __builtin_fmaf(lam, sl[j], v[j]);
         pw = __builtin_fmaf(gv[j], wl[j], pw);
         ps = __builtin_fmaf(gv[j], sl[j], ps);
-        if (GY) {
-          qz[j] = __builtin_fmaf(gv[j], tc.x, qz[j]);
-          ra[j] = __builtin_fmaf(gv[j], tc.y, ra[j]);
+        if (i >= F0) {
+          qz[j] = __builtin_fmaf(gv[j], t.z, qz[j]);
+          ra[j] = __builtin_fmaf(gv[j], t.w, ra[j]);
         }
       }
-      dq = __builtin_fmaf(tz.x, pw, __builtin_fmaf(tz.y, ps, dq));
+      dq = __builtin_fmaf(t.x, pw, __builtin_fmaf(t.y, ps, dq));
       if (i == fin_i) {
 #pragma unroll
         for (int j = 0; j < VW; ++j) dq = __builtin_fmaf(sm.gfin[ds * VW + j], wl[j], dq);
       }
-      tz = tn;
-      tc = cn;
+      t = tn;
       pin(sl);
       pin(wl);
       asm volatile("" : "+v"(dq));
-      if (GY) {
+      if (GY && i >= F0) {
         pin(qz);
         pin(ra);
       }
     }
-    if (GY) add_fin(fin_i, ds, sm, qz, ra);
+    if (F0 == 0) add_fin(fin_i, ds, sm, qz, ra);
   }
 
   // The final-state gradient's share of qz and ra (row fin_i of the lane).
@@ -1111,19 +1112,24 @@ struct ChunkBwd {
     }
   }
 
-  // gy-only sweep: qz = Q1 + sum_i e_i lam^(i+1), ra = gl at the lane's first
-  // row (zero carry from the right) = sum_i lam^i u_i.
+  // gy-only sweep over the lane's rows below F1: qz = Q1 + sum_i e_i
+  // lam^(i+1), ra = gl at the lane's first row (zero carry from the right) =
+  // sum_i lam^i u_i, summed onto the forward sweep's sums of the later rows
+  // (ADD) or from zero.
+  template <int F1, bool ADD>
   __device__ static void sweep_gy(uint4 (&rg)[R], int g, int fin_i, int ds, const Smem& sm, float (&qz)[VW],
                                   float (&ra)[VW]) {
+    if (!ADD) {
 #pragma unroll
-    for (int j = 0; j < VW; ++j) {
-      qz[j] = 0.0f;
-      ra[j] = 0.0f;
+      for (int j = 0; j < VW; ++j) {
+        qz[j] = 0.0f;
+        ra[j] = 0.0f;
+      }
     }
     float2 tc = *reinterpret_cast<const float2*>(&sm.rt4[g * TS].z);
 #pragma unroll
-    for (int i = 0; i < R; ++i) {
-      const float2 tn = *reinterpret_cast<const float2*>(&sm.rt4[g * TS + (i + 1 < R ? i + 1 : i)].z);
+    for (int i = 0; i < F1; ++i) {
+      const float2 tn = *reinterpret_cast<const float2*>(&sm.rt4[g * TS + (i + 1 < F1 ? i + 1 : i)].z);
       float gv[VW];
       opaque(rg[i]);
       unpack16<T>(rg[i], gv);
@@ -1279,19 +1285,20 @@ struct ChunkBwd {
 
     const int fin_i = rc == 0 && a.gfin != nullptr && li >= 0 && gr + li == left ? li : -1;
 
-    // 16 rows per lane hold 128 registers of rows: there the gy-only sums take
-    // a pass of their own (sweep_gy), so as not to hold 16 more registers
+    // 16 rows per lane hold 128 registers of rows: there the forward sweep
+    // takes the gy-only sums of rows 8-15 only, and rows 0-7 get a pass of
+    // their own (sweep_gy) afterwards, so as not to hold 16 more registers
     // while every row is in flight.
-    constexpr bool kFold = R <= 8;
+    constexpr int kF0 = R <= 8 ? 0 : R / 2;
     float sl[VW], wl[VW], dq, qz[VW], ra[VW];
-    sweep_fwd<kFold>(rv, rg, lam, g, fin_i, ds, sm, sl, wl, dq, qz, ra);
+    sweep_fwd<kF0>(rv, rg, lam, g, fin_i, ds, sm, sl, wl, dq, qz, ra);
     // The launch epoch, first needed to publish (below).  Read here, once
     // every row has been consumed: loads complete in order, so waiting for it
     // earlier would have waited for every row (and holding it in a register
     // across the row loads would spill).
     const EpochErr eh = read_epoch_v(a.hdr);
     const unsigned epoch = eh.epoch;
-    if (!kFold) sweep_gy(rg, g, fin_i, ds, sm, qz, ra);
+    if constexpr (kF0 > 0) sweep_gy<kF0, (kF0 < R)>(rg, g, fin_i, ds, sm, qz, ra);
 
     // Scans over the row groups of the wavefront, both directions: sl holds
     // the lane's forward total, ra its reverse total.
