@@ -1051,15 +1051,13 @@ struct ChunkBwd {
   __device__ static void sweep_fwd(const uint4 (&rv)[R], uint4 (&rg)[R], float lam, int g, int fin_i, int ds,
                                    const Smem& sm, float (&sl)[VW], float (&wl)[VW], float& dq, float (&qz)[VW],
                                    float (&ra)[VW]) {
-    constexpr bool GY = F0 < R;
+    static_assert(F0 < R, "the sweep takes the gy-only sums of its last rows at least");
 #pragma unroll
     for (int j = 0; j < VW; ++j) {
       sl[j] = 0.0f;
       wl[j] = 0.0f;
-      if (GY) {
-        qz[j] = 0.0f;
-        ra[j] = 0.0f;
-      }
+      qz[j] = 0.0f;
+      ra[j] = 0.0f;
     }
     dq = 0.0f;
     float4 t = sm.rt4[g * TS];
@@ -1090,7 +1088,7 @@ struct ChunkBwd {
       pin(sl);
       pin(wl);
       asm volatile("" : "+v"(dq));
-      if (GY && i >= F0) {
+      if (i >= F0) {
         pin(qz);
         pin(ra);
       }
@@ -1112,20 +1110,12 @@ struct ChunkBwd {
     }
   }
 
-  // gy-only sweep over the lane's rows below F1: qz = Q1 + sum_i e_i
-  // lam^(i+1), ra = gl at the lane's first row (zero carry from the right) =
-  // sum_i lam^i u_i, summed onto the forward sweep's sums of the later rows
-  // (ADD) or from zero.
-  template <int F1, bool ADD>
+  // gy-only sweep over the lane's rows below F1, summed onto the forward
+  // sweep's sums of the later rows: qz = Q1 + sum_i e_i lam^(i+1), ra = gl at
+  // the lane's first row (zero carry from the right) = sum_i lam^i u_i.
+  template <int F1>
   __device__ static void sweep_gy(uint4 (&rg)[R], int g, int fin_i, int ds, const Smem& sm, float (&qz)[VW],
                                   float (&ra)[VW]) {
-    if (!ADD) {
-#pragma unroll
-      for (int j = 0; j < VW; ++j) {
-        qz[j] = 0.0f;
-        ra[j] = 0.0f;
-      }
-    }
     float2 tc = *reinterpret_cast<const float2*>(&sm.rt4[g * TS].z);
 #pragma unroll
     for (int i = 0; i < F1; ++i) {
@@ -1298,7 +1288,7 @@ struct ChunkBwd {
     // across the row loads would spill).
     const EpochErr eh = read_epoch_v(a.hdr);
     const unsigned epoch = eh.epoch;
-    if constexpr (kF0 > 0) sweep_gy<kF0, (kF0 < R)>(rg, g, fin_i, ds, sm, qz, ra);
+    if constexpr (kF0 > 0) sweep_gy<kF0>(rg, g, fin_i, ds, sm, qz, ra);
 
     // Scans over the row groups of the wavefront, both directions: sl holds
     // the lane's forward total, ra its reverse total.
