@@ -422,6 +422,53 @@ def bench_e2e(torch, dev, iters=5):
         key = "fused_layout" if fused else "reference_glue"
         out[key] = {"ms_per_forward": round(sec * 1e3, 3), "tokens_per_s": round(B * N / sec, 1)}
     out["decay_path_per_layer"] = decay_path_per_layer(torch, dev)
+    out["prefill_with_cache"] = bench_prefill_cache(torch, dev, model, ids)
+    return out
+
+
+def bench_prefill_cache(torch, dev, model, ids, iters=3):
+    """C5 prefill with use_cache: the decay state each layer hands to decoding.
+
+    The reference seeds it after the full-sequence op with an N-step loop of
+    two torch ops per step (attention.py:383-394); here the scan returns it
+    with y from the same launch (return_final_state).  Timed for the whole C5
+    model forward with use_cache (both with the layout-fused op), and for one
+    layer's seed alone at the C5 shape: the loop, against one scan launch that
+    returns y and the state."""
+    import kilat_amd
+    from tests.e2e_model import KernelDecayCache, ReferenceDecayCache
+
+    B, N = ids.shape
+    out = {"config": "C5 model forward with use_cache (B=8 N=1024, bf16 autocast), and one layer's "
+                     "decay-state seed at B=8 N=1024 H=6 D=64 bf16"}
+    for key, ops in (("reference_seed_loop", ReferenceDecayCache()), ("scan_final_state", KernelDecayCache())):
+        model.set_decay(kilat_amd.triton_global_decay, fused_layout=True, cache_ops=ops)
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            model(ids, use_cache=True)
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            for _ in range(iters):
+                model(ids, use_cache=True)
+            torch.cuda.synchronize()
+            sec = (time.perf_counter() - t) / iters
+        out[key] = {"ms_per_prefill": round(sec * 1e3, 3), "tokens_per_s": round(B * N / sec, 1)}
+    model.set_decay(kilat_amd.triton_global_decay, fused_layout=False, cache_ops=ReferenceDecayCache())
+
+    H, D = 6, 64
+    g = torch.Generator(device=dev).manual_seed(7)
+    V = torch.randn(B, H, N, D, generator=g, device=dev).to(torch.bfloat16)
+    lam = c2_lam(H, torch).to(dev)
+    layer = {}
+    for key, ops, reps in (("reference_seed_loop_us", ReferenceDecayCache(), 3),
+                           ("scan_with_final_state_us", KernelDecayCache(), 200)):
+        ops.prefill(kilat_amd.triton_global_decay, lam, V, torch.float32)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(reps):
+            ops.prefill(kilat_amd.triton_global_decay, lam, V, torch.float32)
+        torch.cuda.synchronize()
+        layer[key] = round((time.perf_counter() - t) / reps * 1e6, 2)
+    out["per_layer"] = layer
     return out
 
 
