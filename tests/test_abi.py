@@ -316,6 +316,32 @@ def test_bench_refuses_more_than_one_gpu():
     assert "one GPU" in r.stderr and r.stdout == ""
 
 
+def test_bench_buffer_sets_are_disjoint_and_back_to_back():
+    """bench.py's rotated (V, y) sets: each tensor a contiguous view of one
+    allocation, pairs back to back with no overlap, V seeded and y of the
+    output type (checked on the CPU; the bench carves them on the GPU)."""
+    import bench
+
+    shape, n = (2, 3, 5, 8), 2 * 3 * 5 * 8
+    for ti, to in ((torch.bfloat16, torch.float32), (torch.float16, torch.float16), (torch.float32, torch.float32)):
+        sets = bench.carved_pairs(torch, torch.device("cpu"), shape, ti, to, 3, seed=4)
+        base = sets[0][0].data_ptr()
+        ei, eo = torch.empty(0, dtype=ti).element_size(), torch.empty(0, dtype=to).element_size()
+        for k, (V, y) in enumerate(sets):
+            assert V.dtype == ti and y.dtype == to and V.shape == shape == y.shape
+            assert V.is_contiguous() and y.is_contiguous()
+            assert V.data_ptr() - base == k * n * (ei + eo)
+            assert y.data_ptr() - base == k * n * (ei + eo) + n * ei
+        again = bench.carved_pairs(torch, torch.device("cpu"), shape, ti, to, 3, seed=4)
+        assert all(torch.equal(a[0], b[0]) for a, b in zip(sets, again))
+        assert not torch.equal(sets[0][0], sets[1][0])
+    sets = bench.rotated_sets(torch, torch.device("cpu"), shape, 4)
+    base = sets[0][0].data_ptr()
+    for k, (V, y) in enumerate(sets):
+        assert V.dtype == y.dtype == torch.bfloat16
+        assert V.data_ptr() - base == 2 * k * n * 2 and y.data_ptr() - base == (2 * k + 1) * n * 2
+
+
 def test_integration_doc_holds_the_tested_ctypes_stub():
     """The integration guide's ctypes stub is the text tests/ctypes_stub.py runs on the GPU."""
     from tests.ctypes_stub import STUB_SOURCE
