@@ -841,13 +841,21 @@ struct ChunkScan {
         if (i >= 2) wait_vmcnt<2 * (VW * (int)sizeof(TO) / 16)>();
       }
     };
-    if (nvalid == R && ifin < 0) {
-      // Every row of the lane inside the sequence and none of them row N-1:
-      // no per-row guard (each guard made the compiler merge the state with
-      // copies at its join: B=8 N=4096 H=12 D=64 1.5% and B=8 N=1024 H=6 4%
-      // slower with the guarded loop alone).
+    if (nvalid == R && (ifin < 0 || ifin == R - 1)) {
+      // Every row of the lane inside the sequence and row N-1, if the lane
+      // holds it, its last: no per-row guard (each guard made the compiler
+      // merge the state with copies at its join: B=8 N=4096 H=12 D=64 1.5%
+      // and B=8 N=1024 H=6 4% slower with the guarded loop alone).  The
+      // final state is then the state after the loop.  (Sent down the
+      // guarded loop, the lanes holding row N-1 made their wavefront run
+      // both loops, in the last chunk of every stream: C2 with the final
+      // state 18.7 against 17.5 us without.)
 #pragma unroll
       for (int i = 0; i < R; ++i) row(i);
+      if (ifin == R - 1) {
+#pragma unroll
+        for (int j = 0; j < VW; ++j) a.fin[c0 + ds * VW + j] = st[j];
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < R; ++i) {
@@ -1139,15 +1147,17 @@ struct ChunkBwd {
   // (rows up to li, the lane's last row inside the sequence).
   __device__ static void sweep_dv(const BwdArgs& a, uint4 (&rg)[R], float lam, int g, int li, int fin_i, int ds,
                                   const Smem& sm, T* dp, float (&gn)[VW]) {
-    // Every row of the lane inside the sequence and none of them row N-1: no
-    // per-row guard (C2 29.5 -> 29.3 us, B=1 N=65536 H=16 D=128 146.6 ->
-    // 145.2 us).  Only for full 128-byte channel groups: for narrower ones
-    // the second loop made one of the kernels spill (D=32 bf16, several
-    // rounds, 7% slower).  With 16 rows, at most two rows' stores in flight
-    // per wavefront, as in the forward (C2 29.65 -> 29.18 us, B=24 N=1024
-    // H=16 29.63 -> 29.29 us, same-box A/B; no gain with 4 rows).
+    // Every row of the lane inside the sequence and row N-1, if the lane
+    // holds it, its last (the first this pass takes): no per-row guard (C2
+    // 29.5 -> 29.3 us, B=1 N=65536 H=16 D=128 146.6 -> 145.2 us), one guarded
+    // add of the final-state gradient on the first row.  Only for full
+    // 128-byte channel groups: for narrower ones the second loop made one of
+    // the kernels spill (D=32 bf16, several rounds, 7% slower).  With 16
+    // rows, at most two rows' stores in flight per wavefront, as in the
+    // forward (C2 29.65 -> 29.18 us, B=24 N=1024 H=16 29.63 -> 29.29 us,
+    // same-box A/B; no gain with 4 rows).
     if constexpr (LPR == 8) {
-      if (li == R - 1 && fin_i < 0) {
+      if (li == R - 1 && (fin_i < 0 || fin_i == R - 1)) {
 #pragma unroll
         for (int i = R - 1; i >= 0; --i) {
           float gv[VW];
@@ -1156,6 +1166,10 @@ struct ChunkBwd {
           const float rz = sm.rt4[g * TS + i].x;
 #pragma unroll
           for (int j = 0; j < VW; ++j) gn[j] = __builtin_fmaf(lam, gn[j], gv[j] * rz);
+          if (i == R - 1 && fin_i == R - 1) {
+#pragma unroll
+            for (int j = 0; j < VW; ++j) gn[j] += sm.gfin[ds * VW + j];
+          }
           store_vec<T, VW>(dp + (int64_t)i * a.dn, gn);
           if constexpr (R >= 16) {
             if (i <= R - 3) wait_vmcnt<2>();
