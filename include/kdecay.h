@@ -168,9 +168,11 @@ int kdecay_scan_fwd_sequential(const void* V, int v_dtype,
                                void* stream);
 
 /*
- * Forward scan for training: kdecay_scan_fwd, plus the states the backward
- * pass needs (the state at every kdecay_scan_bwd chunk boundary, so the
- * backward recomputes s inside each chunk without a second look-back).
+ * Forward scan for training: kdecay_scan_fwd, plus what the backward pass
+ * needs: the state at every kdecay_scan_bwd chunk boundary (so the backward
+ * recomputes s inside each chunk without a second look-back), and each row's
+ * 1/z and d(1/z)/dlam for every head (so the backward loads them instead of
+ * computing them before its first row).
  * The reference has no GPU backward (its Triton path returns a tensor with no
  * autograd graph, triton_ops.py:309-330); its CPU path is differentiated by
  * torch autograd through /root/reference/src/kilat/arc/triton_ops.py:240-246.
@@ -189,7 +191,8 @@ int kdecay_scan_fwd_train(const void* V, int v_dtype, const int64_t* v_strides,
                           void* workspace, size_t workspace_bytes,
                           void* stream);
 
-/* Floats of the states buffer kdecay_scan_fwd_train fills (0: none needed). */
+/* Floats of the states buffer kdecay_scan_fwd_train fills (0: none needed):
+ * B*H*D per backward chunk boundary plus 2*H*N row terms. */
 size_t kdecay_scan_saved_states_floats(int64_t B, int64_t H, int64_t N,
                                        int64_t D, int v_dtype);
 
@@ -208,7 +211,9 @@ size_t kdecay_scan_saved_states_floats(int64_t B, int64_t H, int64_t N,
  *                row) x 16 rows: 512 rows for a 128-byte channel group (D >=
  *                64 bf16/fp16, D >= 32 fp32), 1024 for 64 bytes, 2048 for 32
  *                bytes; a quarter of that for small grids.
- *   lam, init_state, t_offset   as given to the forward call
+ *   lam, init_state, t_offset   as given to the forward call (the row terms
+ *                come from the states buffer, computed with the forward's
+ *                lam and t_offset)
  *   states       the forward call's states (NULL allowed when
  *                kdecay_scan_saved_states_floats() is 0)
  *   g_final      nullable fp32 [B,H,D]: gradient of the forward's final state

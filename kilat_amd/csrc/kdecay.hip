@@ -479,6 +479,10 @@ struct ScanArgs {
   float* states;
   int64_t state_rows;
   int64_t nsaved;
+  // With the states: the backward's terms of every row of every head,
+  // rowtab[h * N + t] = (1/z, d(1/z)/dlam) at row t (bwd_row_terms), written
+  // by the streams of batch 0, first channel group.
+  float2* rowtab;
   int spin_limit;  // polls before a look-back gives up (kSpinLimit unless a test lowers it)
   FastDiv f_nstream, f_ng, f_H;  // division by nstream, ng and H
 };
@@ -588,6 +592,24 @@ __device__ __forceinline__ Pos pos_of(const ScanArgs& a, int item) {
 // Items are numbered chunk-major (item = chunk * nstream + j, j rotated to
 // the stream by the chunk index; see rotated_stream), so the chunk an item
 // waits on always has a smaller item number.
+// The backward's terms of one row with exponent e = t + 1, from p = lam^(e-1):
+//   x = 1/z = ((1 - lam) + 1e-6) / (1 - lam^e)   (lam^e as z_of takes it)
+//   y = d(1/z)/dlam = (e lam^(e-1) ((1 - lam) + 1e-6) - (1 - lam^e)) / (1 - lam^e)^2
+// lam^e is p times lam (in double); y's numerator, a small difference of
+// nearly equal terms when lam is close to 1, stays in double, and both
+// quotients are fp32 divisions.  (Two double-precision power loops and a
+// double division per row were most of the table's cost; it is built by
+// every workgroup for its chunk's rows, on the critical path after the rows
+// arrive.)
+__device__ __forceinline__ void bwd_row_terms(float lam, int64_t e, double p, float& x, float& y) {
+  const double l = lam;
+  const double pe = p * l;
+  const float pf = e == 1 ? lam : e == 2 ? lam * lam : e == 3 ? (lam * lam) * lam : (float)pe;
+  x = ((1.0f - lam) + 1e-6f) / (1.0f - pf);
+  const double A = 1.0 - pe;
+  y = (float)((double)e * p * ((1.0 - l) + 1e-6) - A) / (float)(A * A);
+}
+
 template <typename TI, typename TO, int LPR, int R, int NW, int W, bool FZ, bool THR>
 struct ChunkScan {
   static constexpr int VW = 16 / (int)sizeof(TI);  // channels per lane
@@ -736,6 +758,21 @@ struct ChunkScan {
         if (d < DG) {
           if (multi && !last) publish(base + (int64_t)chunk * DG + d, tag_inc, __builtin_fmaf(mL, carry[q], agg[q]));
           sm.carry[d] = carry[q];
+        }
+      }
+    }
+    // Training forward: the backward's terms of this chunk's rows, once per
+    // head, by the other wavefronts while wavefront 0 looks back.
+    if constexpr (NW > 1) {
+      if (a.rowtab && p.b == 0 && grp == 0 && wave > 0) {
+        for (int r = tid - 64; r < L; r += NT - 64) {
+          const int64_t row = row0 + r;
+          if (row < a.N) {
+            const int64_t t = a.t_offset + row;
+            float x, y;
+            bwd_row_terms(lam, t + 1, ipow_f64((double)lam, t), x, y);
+            a.rowtab[p.h * a.N + row] = make_float2(x, y);
+          }
         }
       }
     }
@@ -946,6 +983,7 @@ struct BwdArgs {
   const float* lam;
   const float* init;    // [B*H*D] or null
   const float* states;  // forward states at chunk starts (ScanArgs::states layout), null if nchunk == 1
+  const float2* rowtab; // the training forward's per-row terms (ScanArgs::rowtab), null if nchunk == 1
   const float* gfin;    // [B*H*D] or null: gradient of the final state
   float* dinit;         // [B*H*D] or null
   float* dlam;          // [H]
@@ -965,24 +1003,6 @@ struct BwdArgs {
 // XCDs of the device: workgroups are handed to them round-robin by index, and
 // each XCD dispatches its share in index order.
 constexpr int kXcds = 8;
-
-// The backward's terms of one row with exponent e = t + 1, from p = lam^(e-1):
-//   x = 1/z = ((1 - lam) + 1e-6) / (1 - lam^e)   (lam^e as z_of takes it)
-//   y = d(1/z)/dlam = (e lam^(e-1) ((1 - lam) + 1e-6) - (1 - lam^e)) / (1 - lam^e)^2
-// lam^e is p times lam (in double); y's numerator, a small difference of
-// nearly equal terms when lam is close to 1, stays in double, and both
-// quotients are fp32 divisions.  (Two double-precision power loops and a
-// double division per row were most of the table's cost; it is built by
-// every workgroup for its chunk's rows, on the critical path after the rows
-// arrive.)
-__device__ __forceinline__ void bwd_row_terms(float lam, int64_t e, double p, float& x, float& y) {
-  const double l = lam;
-  const double pe = p * l;
-  const float pf = e == 1 ? lam : e == 2 ? lam * lam : e == 3 ? (lam * lam) * lam : (float)pe;
-  x = ((1.0f - lam) + 1e-6f) / (1.0f - pf);
-  const double A = 1.0 - pe;
-  y = (float)((double)e * p * ((1.0 - l) + 1e-6) - A) / (float)(A * A);
-}
 
 // Value of `x` held K row groups above (row groups S lanes apart; lanes with
 // gw + K >= GW get an unspecified value).
@@ -1018,6 +1038,16 @@ struct ChunkBwd {
   static constexpr int L = G * R;
   static constexpr int NT = NW * 64;
   static constexpr int DQ = (DG + 63) / 64;
+  static constexpr int NR = (L + NT - 1) / NT;  // rows of the table per thread
+  // Load the training forward's row terms (BwdArgs::rowtab) instead of
+  // computing them, for 2 rows per thread (16 rows per lane, 128-byte
+  // channel groups): the table's power and division chain then no longer
+  // delays the first sweep row (C2 28.1-28.3 -> 27.3-27.6 us, B=24 N=1024
+  // H=16 27.8 -> 27.5, C4 145.0 either way, gradients bit-identical;
+  // same-box A/B).  With 4 rows per thread (D=32 bf16) the eight loads cost
+  // more than the chain (25.6 -> 26.4 us), with 1 (128-row chunks) the table
+  // is short already (13.5 -> 13.6 us), and with 8 their registers spilled.
+  static constexpr bool kLoadTerms = NR == 2;
   static_assert(G + 1 <= NT, "power table is filled one entry per thread");
 
   // Per row of the chunk (i = the row's index in its lane, 0 <= i < R):
@@ -1232,6 +1262,17 @@ struct ChunkBwd {
       if (chunk == 0 && !a.init) cs = 0.0f;
       if (!fin) cf = 0.0f;
     }
+    // The row terms the training forward saved for this thread's rows of the
+    // table (below), loaded before the rows so that they arrive first; rows
+    // past the end read row N-1, and without saved terms a.lam stands in.
+    float tx[NR], ty[NR];
+#pragma unroll
+    for (int k = 0; k < (kLoadTerms ? NR : 0); ++k) {
+      const int64_t r = row0 + tid + k * NT < a.N ? row0 + tid + k * NT : a.N - 1;
+      const float* tp = a.rowtab ? reinterpret_cast<const float*>(a.rowtab + h * a.N + r) : a.lam;
+      tx[k] = tp[0];
+      ty[k] = (a.rowtab ? tp + 1 : a.lam)[0];
+    }
 
     // Rows of V and gy, through buffer loads whose range ends with the
     // stream's row N-1: rows past the end read as zero (the hardware's range
@@ -1268,17 +1309,30 @@ struct ChunkBwd {
       const int i = tid % R;
       const float p = pow_like_torch(lam, i);
       const float p1 = p * lam;
-      double q = ipow_f64((double)lam, a.t_offset + row0 + tid);
-      double step = lam;
+      if (kLoadTerms && a.rowtab) {
 #pragma unroll
-      for (int k = 0; k < ilog2(NT); ++k) step *= step;
-      for (int r = tid; r < L; r += NT) {
-        const int64_t t = a.t_offset + row0 + r;
-        float x = 0.0f, y = 0.0f;
-        if (row0 + r < a.N) bwd_row_terms(lam, t + 1, q, x, y);
-        const float w = x * p;
-        sm.rt4[r + r / R] = make_float4(x, y, __builtin_fmaf(w, (float)(i + 1), y * p1), w);
-        q *= step;
+        for (int k = 0; k < NR; ++k) {
+          const int r = tid + k * NT;
+          if (r < L) {
+            const bool in = row0 + r < a.N;
+            const float x = in ? tx[k] : 0.0f, y = in ? ty[k] : 0.0f;
+            const float w = x * p;
+            sm.rt4[r + r / R] = make_float4(x, y, __builtin_fmaf(w, (float)(i + 1), y * p1), w);
+          }
+        }
+      } else {
+        double q = ipow_f64((double)lam, a.t_offset + row0 + tid);
+        double step = lam;
+#pragma unroll
+        for (int k = 0; k < ilog2(NT); ++k) step *= step;
+        for (int r = tid; r < L; r += NT) {
+          const int64_t t = a.t_offset + row0 + r;
+          float x = 0.0f, y = 0.0f;
+          if (row0 + r < a.N) bwd_row_terms(lam, t + 1, q, x, y);
+          const float w = x * p;
+          sm.rt4[r + r / R] = make_float4(x, y, __builtin_fmaf(w, (float)(i + 1), y * p1), w);
+          q *= step;
+        }
       }
     }
     if (tid < DG) {
@@ -2219,6 +2273,7 @@ static int scan_fwd_impl(const void* V, int v_dtype, const int64_t* v_strides, v
   a.state_rows = bwd_chunk_rows(B, H, N, D, v_dtype);
   a.nsaved = (N + a.state_rows - 1) / a.state_rows;
   a.states = a.nsaved > 1 ? states : nullptr;
+  a.rowtab = a.states ? reinterpret_cast<float2*>(states + B * H * D * a.nsaved) : nullptr;
 
   if (v_dtype == KDECAY_F32) return dispatch_dg<float, float>(a, DG, grid, s, shape);
   if (v_dtype == KDECAY_BF16) {
@@ -2263,7 +2318,9 @@ size_t kdecay_scan_saved_states_floats(int64_t B, int64_t H, int64_t N, int64_t 
   const int64_t Lb = bwd_chunk_rows(B, H, N, D, v_dtype);
   const int64_t nsaved = (N + Lb - 1) / Lb;
   if (nsaved <= 1) return 0;
-  return (size_t)(B * H * D * nsaved);
+  // The states at the backward's chunk starts, then the backward's two terms
+  // of every row of every head (ScanArgs::rowtab).
+  return (size_t)(B * H * D * nsaved + 2 * H * N);
 }
 
 int kdecay_scan_fwd_train(const void* V, int v_dtype, const int64_t* v_strides, void* out, int out_dtype,
@@ -2366,6 +2423,7 @@ int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides, const 
   a.nchunk = (int)nchunk;
   a.nstream = (int)nstream;
   a.nsaved = nchunk;
+  a.rowtab = nchunk > 1 ? reinterpret_cast<const float2*>(states + B * H * D * nchunk) : nullptr;
   a.f_nstream = make_fastdiv((uint32_t)nstream);
   a.f_ng = make_fastdiv((uint32_t)a.ng);
   a.f_H = make_fastdiv((uint32_t)H);

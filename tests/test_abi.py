@@ -111,6 +111,19 @@ def test_backward_workspace_bytes(kdecay_lib):
     assert wb(2, 6, 100, 48, _lib.KDECAY_BF16) == 0  # unsupported D
 
 
+def test_saved_states_floats(kdecay_lib):
+    """The training forward's buffer for the backward: the state at each backward
+    chunk boundary (B*H*D per chunk of rows) followed by two row terms (1/z and
+    d(1/z)/dlam) per row of every head; nothing when the backward has one chunk."""
+    sf = kdecay_lib.kdecay_scan_saved_states_floats
+    assert sf(8, 12, 4096, 64, _lib.KDECAY_BF16) == 8 * 12 * 64 * (4096 // 512) + 2 * 12 * 4096
+    assert sf(8, 6, 1024, 64, _lib.KDECAY_BF16) == 8 * 6 * 64 * (1024 // 128) + 2 * 6 * 1024  # 128-row chunks
+    assert sf(8, 12, 2049, 64, _lib.KDECAY_BF16) == 8 * 12 * 64 * 5 + 2 * 12 * 2049  # ragged last chunk
+    assert sf(1, 16, 65536, 128, _lib.KDECAY_BF16) == 16 * 128 * (65536 // 512) + 2 * 16 * 65536
+    assert sf(2, 6, 100, 64, _lib.KDECAY_BF16) == 0  # one chunk per stream
+    assert sf(2, 6, 4096, 48, _lib.KDECAY_BF16) == 0  # unsupported D
+
+
 def _scan(lib, v_dtype=_lib.KDECAY_BF16, out_dtype=None, D=64, N=4096, vstr=None, ostr=None,
           V=FAKE, out=FAKE, ws=None, wsb=0):
     out_dtype = v_dtype if out_dtype is None else out_dtype
