@@ -214,15 +214,18 @@ def test_backward_init_final_offset(hip_device, kdecay_lib):
     check(dv, dl, di, rdv, rdl, rdi, torch.float32, "init+gfin+offset")
 
 
-@pytest.mark.parametrize("dname", ["f32", "bf16"])
-def test_backward_init_final_offset_large_grid(hip_device, kdecay_lib, dname):
+@pytest.mark.parametrize("dname,N", [("f32", 2600), ("bf16", 2600), ("bf16", 2560)])
+def test_backward_init_final_offset_large_grid(hip_device, kdecay_lib, dname, N):
     """Carry-in state, final-state gradient and position offset on grids of
     more than 512 forward chunks at 512 rows (576 bf16, 1152 f32: the 16-row
     forward kernel) and 2016/4032 backward chunks, against the fp64 adjoint
-    recurrence."""
+    recurrence.  N = 2600 ends inside a lane's rows (the guarded loops);
+    N = 2560 (five 512-row backward chunks per stream, 480 in all: the 16-row
+    backward kernel) ends on a lane's last row, where the forward writes the
+    final state and the backward adds its gradient on the unguarded loops."""
     dtype = DTYPES[dname]
     g = torch.Generator().manual_seed(212)
-    B, H, N, D = 12, 8, 2600, 64
+    B, H, D = 12, 8, 64
     lam = lam_uniform(H, 0.8, 0.9999, g)
     V = torch.randn(B, H, N, D, generator=g).to(dtype)
     gy = torch.randn(B, H, N, D, generator=g).to(dtype)
@@ -230,7 +233,7 @@ def test_backward_init_final_offset_large_grid(hip_device, kdecay_lib, dname):
     gfin = torch.randn(B, H, D, generator=g)
     dv, dl, di = gpu_grads(lam, V, gy, hip_device, init=init, gfin=gfin, t_offset=33)
     rdv, rdl, rdi = O.scan_grads_f64(lam, V, gy, init_state=init, gfin=gfin, t_offset=33)
-    check(dv, dl, di, rdv, rdl, rdi, dtype, f"large grid {dname}")
+    check(dv, dl, di, rdv, rdl, rdi, dtype, f"large grid {dname} N={N}")
 
 
 @pytest.mark.parametrize("dname,B,H,N,D", [("bf16", 8, 12, 2048, 64), ("bf16", 8, 12, 2049, 64),
