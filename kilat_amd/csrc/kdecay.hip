@@ -1069,7 +1069,7 @@ struct ChunkBwd {
     float carry_s[DG]; // state before the chunk's first row
     float carry_g[DG]; // g after the chunk's last row
     float gfin[DG];    // final-state gradient (last chunk only; zero elsewhere)
-    float red[NW];     // carry-free dlam partial per wavefront
+    double red[NW];    // carry-free dlam partial per wavefront
   };
 
   // Forward sweep over V and gy together (zero state in): sl = lane-local
@@ -1425,11 +1425,19 @@ struct ChunkBwd {
 
     // s_in (true, from the saved chunk state) and g_out without the chunk's
     // carry; the carry-free part of the lane's dlam, and K per channel.
+    // From here the chunk's dlam partial is summed in double (the lane's
+    // channel terms, the wavefront and workgroup sums, the carry term): dlam
+    // is often a small remainder of large terms of both signs, and in fp32
+    // these sums lost most of its digits (B=45 H=1 N=1388 D=128 bf16, 8 M
+    // terms for one head: relative error 1.9e-4 against 1.9e-6 in double,
+    // and 1.3e-4 for the reference's own fp32 path; C2 unchanged, C4 and the
+    // small grids 0.7-1.3% slower).  The lane's row sums (dq) stay fp32: in
+    // double they took the registers of the narrow-group kernels.
     const float mg = sm.pw[g], mgw = sm.pw[gw];
     const float mr = sm.pw[G - 1 - g], mrw = sm.pw[GW - 1 - gw];
     const float rlr = (float)R * sm.pw[1];
     float gh0[VW];
-    float dsum = dq;
+    double dsum = dq;
     {
       float ew[VW], er[VW];
 #pragma unroll
@@ -1450,33 +1458,33 @@ struct ChunkBwd {
         const float sin = __builtin_fmaf(mg, sm.carry_s[ds * VW + j], __builtin_fmaf(mgw, ew[j], xin[j]));
         gh0[j] = __builtin_fmaf(mrw, er[j], rin[j]);
         const float x = __builtin_fmaf(sin, rlr, lam * wl[j]);  // Q2 + s_in R lam^R
-        dsum = __builtin_fmaf(gh0[j], x, __builtin_fmaf(sin, qz[j], dsum));
+        dsum = __builtin_fma((double)gh0[j], (double)x, __builtin_fma((double)sin, (double)qz[j], dsum));
         sm.kq[g][ds * VW + j] = mr * x;
       }
     }
-    dsum = wave_sum(dsum);
+    dsum = wave_sum_f64(dsum);
     if (lane == 0) sm.red[wave] = dsum;
     __syncthreads();  // carry_g, kq, red
 
     // The chunk's dlam partial: the carry-free part plus carry * K.
     if (wave == 0) {
-      float e = 0.0f;
+      double e = 0.0;
 #pragma unroll
       for (int q = 0; q < DQ; ++q) {
         const int d = lane + 64 * q;
         if (d < DG) {
-          float kc = 0.0f;
+          double kc = 0.0;
 #pragma unroll
-          for (int r = 0; r < G; ++r) kc += sm.kq[r][d];
-          e = __builtin_fmaf(cg[q], kc, e);
+          for (int r = 0; r < G; ++r) kc += (double)sm.kq[r][d];
+          e = __builtin_fma((double)cg[q], kc, e);
         }
       }
-      e = wave_sum(e);
+      e = wave_sum_f64(e);
       if (lane == 0) {
-        float sum = e;
+        double sum = e;
 #pragma unroll
         for (int w = 0; w < NW; ++w) sum += sm.red[w];
-        publish(a.partial + (int64_t)rc * a.nstream + stream, tag_of(epoch, 0u), sum);
+        publish(a.partial + (int64_t)rc * a.nstream + stream, tag_of(epoch, 0u), (float)sum);
       }
     }
 
