@@ -286,6 +286,24 @@ def test_backward_fp32_lambda_near_one(hip_device, kdecay_lib):
     assert rel(dl, rdl) <= 1e-4, f"dlam rel {rel(dl, rdl):.3e}"
 
 
+def test_backward_dlam_one_head_many_terms(hip_device, kdecay_lib):
+    """dlam of a single head summed over 45 x 1388 x 128 = 8 M terms of both
+    signs (bf16, a random parity sweep's case): its value, -2.636, is a small
+    remainder of the terms, so the sums' precision decides its digits.  The
+    reference's fp32 path is 1.3e-4 off the fp64 adjoint here; the chunk
+    partials summed in fp32 were 1.9e-4 off, summed in double 1.9e-6."""
+    B, H, N, D = 45, 1, 1388, 128
+    g = torch.Generator().manual_seed(937 + 50000)
+    lam = (0.3 + (0.9999 - 0.3) * torch.rand(H, generator=g)).float()
+    V = torch.randn(B, H, N, D, generator=g).to(torch.bfloat16)
+    gy = torch.randn(B, H, N, D, generator=g).to(torch.bfloat16)
+    print(f"  dlam over one head: bf16 {B}x{H}x{N}x{D}", flush=True)
+    dv, dl, _ = gpu_grads(lam, V, gy, hip_device)
+    rdv, rdl, _ = O.scan_grads_f64(lam, V, gy)
+    assert rel(dl, rdl) <= 2e-5, f"dlam rel {rel(dl, rdl):.3e}"
+    check(dv, dl, None, rdv, rdl, None, torch.bfloat16, "one head")
+
+
 def test_backward_dlam_cancellation(hip_device, kdecay_lib):
     """dlam as a difference of two nearly equal sums (a random parity sweep's
     case: bf16 B=3 H=1 N=1534 D=128 with carry-in, final-state gradient and
