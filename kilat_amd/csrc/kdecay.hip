@@ -474,8 +474,10 @@ struct ScanArgs {
   u64* flags;   // [nstream][nchunk][DG] look-back words (null if nchunk == 1)
   unsigned* hdr;
   // Optional: the state after every `state_rows` rows, for the backward pass.
-  // states[(stream * nsaved + k) * DG + c] = s at row k * state_rows - 1
-  // (1 <= k < nsaved = ceil(N / state_rows); entry 0 is not written).
+  // states[(bh * nsaved + k) * D + d] = s of channel d of head bh at row
+  // k * state_rows - 1 (1 <= k < nsaved = ceil(N / state_rows); entry 0 is
+  // not written): by head and channel, so the backward may group a head's
+  // channels into streams other than the forward's.
   float* states;
   int64_t state_rows;
   int64_t nsaved;
@@ -908,7 +910,7 @@ struct ChunkScan {
     if (a.states) {
       const int64_t e = rbase + R;  // st is the state at row e - 1
       if (e < a.N && e % a.state_rows == 0) {
-        float* sp = a.states + ((int64_t)stream * a.nsaved + e / a.state_rows) * DG + ds * VW;
+        float* sp = a.states + ((int64_t)bh * a.nsaved + e / a.state_rows) * a.D + grp * DG + ds * VW;
 #pragma unroll
         for (int j = 0; j < VW; ++j) sp[j] = st[j];
       }
@@ -982,7 +984,7 @@ struct BwdArgs {
   void* dv;
   const float* lam;
   const float* init;    // [B*H*D] or null
-  const float* states;  // forward states at chunk starts (ScanArgs::states layout), null if nchunk == 1
+  const float* states;  // forward states at chunk starts (ScanArgs::states layout, by head and channel), null if nchunk == 1
   const float2* rowtab; // the training forward's per-row terms (ScanArgs::rowtab), null if nchunk == 1
   const float* gfin;    // [B*H*D] or null: gradient of the final state
   float* dinit;         // [B*H*D] or null
@@ -1180,13 +1182,13 @@ struct ChunkBwd {
     // Every row of the lane inside the sequence and row N-1, if the lane
     // holds it, its last (the first this pass takes): no per-row guard (C2
     // 29.5 -> 29.3 us, B=1 N=65536 H=16 D=128 146.6 -> 145.2 us), one guarded
-    // add of the final-state gradient on the first row.  Only for full
-    // 128-byte channel groups: for narrower ones the second loop made one of
-    // the kernels spill (D=32 bf16, several rounds, 7% slower).  With 16
+    // add of the final-state gradient on the first row.  Only for channel
+    // groups of 128 bytes or more: for narrower ones the second loop made one
+    // of the kernels spill (D=32 bf16, several rounds, 7% slower).  With 16
     // rows, at most two rows' stores in flight per wavefront, as in the
     // forward (C2 29.65 -> 29.18 us, B=24 N=1024 H=16 29.63 -> 29.29 us,
     // same-box A/B; no gain with 4 rows).
-    if constexpr (LPR == 8) {
+    if constexpr (LPR >= 8) {
       if (li == R - 1 && (fin_i < 0 || fin_i == R - 1)) {
 #pragma unroll
         for (int i = R - 1; i >= 0; --i) {
@@ -1253,7 +1255,7 @@ struct ChunkBwd {
     float cs, cf;
     {
       const int dc = tid < DG ? tid : DG - 1;
-      const float* cp = chunk > 0 ? a.states + ((int64_t)stream * a.nsaved + chunk) * DG + dc
+      const float* cp = chunk > 0 ? a.states + ((int64_t)bh * a.nsaved + chunk) * a.D + grp * DG + dc
                                   : (a.init ? a.init + c0 + dc : a.lam);
       const bool fin = rc == 0 && a.gfin != nullptr;
       const float* fp = fin ? a.gfin + c0 + dc : a.lam;
@@ -1801,6 +1803,25 @@ int64_t group_width(int v_dtype, int64_t D) {
   return D < full ? D : full;
 }
 
+// Channels of one backward stream: whole 256-byte rows (16 lanes per row,
+// 256-row chunks) for 2-byte heads with a multiple of 128 channels when the
+// grid is large and its chains short, else group_width.  Halves of 256-byte
+// rows read by two streams each made the backward's two-round launches
+// slower than its one-round ones.  Measured (bf16 D=128, same-box A/B on
+// shared buffers, us, 128-byte / 256-byte groups): B=8 N=4096 H=12 (two
+// rounds at 128 bytes; chains of 16 at 256 rows) 65.5 / 61.0; B=4 N=4096
+// H=12 30.8 / 29.9; but B=1 N=65536 H=16 (chains of 256) 145.7 / 165.9 and
+// B=8 N=1024 H=6 (a small grid, 128-row chunks at 128 bytes) 12.6 / 13.6.
+constexpr int64_t kWideChain = 32;  // chunks of 256 rows per stream, at most
+constexpr int64_t kWideGrid = 512;  // chunks of 256 rows in all, at least
+int64_t bwd_group_width(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
+  if (elem_size(v_dtype) == 2 && D % 128 == 0) {
+    const int64_t chain = (N + 255) / 256;
+    if (chain <= kWideChain && chain * B * H * (D / 128) >= kWideGrid) return 128;
+  }
+  return group_width(v_dtype, D);
+}
+
 // Chunk shape: R rows per lane, NW wavefronts per workgroup; `six`: the
 // 8-row grid built for six workgroups per compute unit (see chunk_shape).
 struct ChunkShape {
@@ -2042,7 +2063,7 @@ constexpr int64_t kBwdShortChainGrid = 384;
 // 24.5 / 28.6; D=32 B=8 N=4096 H=16 (512, 4) 32.4 / 29.8.
 int bwd_rows_per_lane(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   const int64_t vw = 16 / elem_size(v_dtype);
-  const int64_t DG = group_width(v_dtype, D);
+  const int64_t DG = bwd_group_width(B, H, N, D, v_dtype);
   const int64_t L = kNWB * (64 / (DG / vw)) * kRB;
   const int64_t nstream = B * H * (D / DG);
   const int64_t chain = (N + L - 1) / L;
@@ -2052,7 +2073,7 @@ int bwd_rows_per_lane(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
 
 int64_t bwd_chunk_rows(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   const int64_t vw = 16 / elem_size(v_dtype);
-  const int64_t lpr = group_width(v_dtype, D) / vw;
+  const int64_t lpr = bwd_group_width(B, H, N, D, v_dtype) / vw;
   return kNWB * (64 / lpr) * bwd_rows_per_lane(B, H, N, D, v_dtype);
 }
 
@@ -2071,6 +2092,10 @@ int launch_bwd(const BwdArgs& a, int64_t grid, int R, hipStream_t s) {
                     : a.nchunk > 8                  ? scan_bwd<T, LPR, kRB, kNWB, 8, 3>
                                                     : one_round;
     hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(kNWB * 64), 0, s, a);
+  } else if constexpr (LPR >= 16) {
+    // Whole 256-byte rows only on large grids (bwd_group_width), which take
+    // 16 rows per lane.
+    return fail(KDECAY_ESHAPE, "no small-grid kernel for %d-channel groups", DG);
   } else {
     // Small grids: by chain length when the grid is resident, as for the
     // forward's small grids.  Measured (bf16 D=64, same-box A/B, window 2 /
@@ -2099,6 +2124,9 @@ int dispatch_bwd(const BwdArgs& a, int64_t DG, int64_t grid, int R, hipStream_t 
     case 32: return launch_bwd<T, 32>(a, grid, R, s);
     case 64:
       if constexpr (sizeof(T) == 2) return launch_bwd<T, 64>(a, grid, R, s);
+      break;
+    case 128:  // whole 256-byte rows (bwd_group_width): 16-row chunks only
+      if constexpr (sizeof(T) == 2) return launch_bwd<T, 128>(a, grid, R, s);
       break;
   }
   return fail(KDECAY_ESHAPE, "unsupported channel group %lld", (long long)DG);
@@ -2348,7 +2376,7 @@ size_t kdecay_scan_bwd_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t 
   const int64_t Lb = bwd_chunk_rows(B, H, N, D, v_dtype);
   const int64_t nchunk = (N + Lb - 1) / Lb;
   const size_t flags = nchunk > 1 ? (size_t)(B * H * nchunk * D) * sizeof(u64) : 0;
-  const int64_t nstream = B * H * (D / group_width(v_dtype, D));
+  const int64_t nstream = B * H * (D / bwd_group_width(B, H, N, D, v_dtype));
   const size_t partial = ((size_t)(nstream * nchunk) * sizeof(u64) + 255) & ~(size_t)255;
   return kHeaderBytes + flags + partial;
 }
@@ -2388,7 +2416,7 @@ int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides, const 
   const int RB = bwd_rows_per_lane(B, H, N, D, v_dtype);
   const int64_t Lb = bwd_chunk_rows(B, H, N, D, v_dtype);
   const int64_t nchunk = (N + Lb - 1) / Lb;
-  const int64_t DG = group_width(v_dtype, D);
+  const int64_t DG = bwd_group_width(B, H, N, D, v_dtype);
   const int64_t nstream = B * H * (D / DG);
   const int64_t grid = nchunk * nstream;
   if (grid > 0x7fffffffLL) return fail(KDECAY_EINVAL, "problem too large (%lld chunks)", (long long)grid);

@@ -96,7 +96,8 @@ def _bwd_rows_fit(t: torch.Tensor) -> bool:
     rows must span less than 2^31 bytes (the library rejects other row
     strides).  A chunk holds at most 4 wavefronts x (64 lanes / lanes per
     row) x 16 rows per lane; the bound below uses that largest chunk, so a
-    tensor that passes is accepted whatever chunk size the library picks."""
+    tensor that passes is accepted whatever chunk size the library picks
+    (whole 256-byte rows, 16 lanes each, make 256-row chunks: fewer rows)."""
     B, H, N, D = t.shape
     es = t.element_size()
     lanes_per_row = min(D, 128 // es) * es // 16

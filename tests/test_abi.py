@@ -109,6 +109,16 @@ def test_backward_workspace_bytes(kdecay_lib):
     # one chunk per stream: no look-back words, but the header and the partials
     assert wb(2, 6, 100, 64, _lib.KDECAY_BF16) == 256 + 256
     assert wb(2, 6, 100, 48, _lib.KDECAY_BF16) == 0  # unsupported D
+    # 128 bf16 channels on a large grid with short chains: whole 256-byte rows,
+    # one stream per head, 256-row chunks (16 per stream, 1536 in all)
+    nst, nch = 8 * 12, 4096 // 256
+    assert wb(8, 12, 4096, 128, _lib.KDECAY_BF16) == 256 + nst * nch * 128 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    # long chains (256 of 256 rows): two 128-byte streams per head, 512-row chunks
+    nst, nch = 1 * 16 * 2, 65536 // 512
+    assert wb(1, 16, 65536, 128, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    # a grid of 256-row chunks below 512 (4 x 6 x 16 = 384): two streams, 512-row chunks
+    nst, nch = 4 * 6 * 2, 4096 // 512
+    assert wb(4, 6, 4096, 128, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
 
 
 def test_saved_states_floats(kdecay_lib):
@@ -120,6 +130,7 @@ def test_saved_states_floats(kdecay_lib):
     assert sf(8, 6, 1024, 64, _lib.KDECAY_BF16) == 8 * 6 * 64 * (1024 // 128) + 2 * 6 * 1024  # 128-row chunks
     assert sf(8, 12, 2049, 64, _lib.KDECAY_BF16) == 8 * 12 * 64 * 5 + 2 * 12 * 2049  # ragged last chunk
     assert sf(1, 16, 65536, 128, _lib.KDECAY_BF16) == 16 * 128 * (65536 // 512) + 2 * 16 * 65536
+    assert sf(8, 12, 4096, 128, _lib.KDECAY_BF16) == 8 * 12 * 128 * (4096 // 256) + 2 * 12 * 4096  # whole rows
     assert sf(2, 6, 100, 64, _lib.KDECAY_BF16) == 0  # one chunk per stream
     assert sf(2, 6, 4096, 48, _lib.KDECAY_BF16) == 0  # unsupported D
 

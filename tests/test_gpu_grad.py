@@ -13,6 +13,7 @@ import pytest
 import torch
 
 import kilat_amd
+from kilat_amd import _lib
 from oracle import decay_oracle as O
 from tests.decay_cases import lam_uniform, rel_err
 
@@ -234,6 +235,32 @@ def test_backward_init_final_offset_large_grid(hip_device, kdecay_lib, dname, N)
     dv, dl, di = gpu_grads(lam, V, gy, hip_device, init=init, gfin=gfin, t_offset=33)
     rdv, rdl, rdi = O.scan_grads_f64(lam, V, gy, init_state=init, gfin=gfin, t_offset=33)
     check(dv, dl, di, rdv, rdl, rdi, dtype, f"large grid {dname} N={N}")
+
+
+@pytest.mark.parametrize("dname,B,H,N,D", [("bf16", 4, 12, 4096, 128), ("f16", 3, 8, 3000, 256),
+                                             ("bf16", 3, 12, 4100, 128)])
+def test_backward_whole_row_streams(hip_device, kdecay_lib, dname, B, H, N, D):
+    """Heads of 128 or 256 bf16/fp16 channels on large grids with short chains:
+    the backward takes whole 256-byte rows per stream (16 lanes per row,
+    256-row chunks; 768, 576 and 612 chunks here), while the forward keeps
+    128-byte groups, so the saved chunk states are read by head and channel.
+    N = 3000 and 4100 end inside a chunk.  Carry-in, final-state gradient and
+    offset, against the fp64 adjoint recurrence."""
+    dtype = DTYPES[dname]
+    code = {"bf16": _lib.KDECAY_BF16, "f16": _lib.KDECAY_F16}[dname]
+    nst, nch = B * H * (D // 128), (N + 255) // 256  # one stream per 128 channels, 256-row chunks
+    assert kdecay_lib.kdecay_scan_bwd_workspace_bytes(B, H, N, D, code) == \
+        256 + nst * nch * 128 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    g = torch.Generator().manual_seed(230 + D + N)
+    lam = lam_uniform(H, 0.5, 0.9999, g)
+    V = torch.randn(B, H, N, D, generator=g).to(dtype)
+    gy = torch.randn(B, H, N, D, generator=g).to(dtype)
+    init = torch.randn(B, H, D, generator=g)
+    gfin = torch.randn(B, H, D, generator=g)
+    print(f"  whole-row backward {dname} {B}x{H}x{N}x{D}", flush=True)
+    dv, dl, di = gpu_grads(lam, V, gy, hip_device, init=init, gfin=gfin, t_offset=21)
+    rdv, rdl, rdi = O.scan_grads_f64(lam, V, gy, init_state=init, gfin=gfin, t_offset=21)
+    check(dv, dl, di, rdv, rdl, rdi, dtype, f"whole rows {dname} {B}x{H}x{N}x{D}")
 
 
 @pytest.mark.parametrize("dname,B,H,N,D", [("bf16", 8, 12, 2048, 64), ("bf16", 8, 12, 2049, 64),
