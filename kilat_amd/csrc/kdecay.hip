@@ -1042,14 +1042,15 @@ struct ChunkBwd {
   static constexpr int DQ = (DG + 63) / 64;
   static constexpr int NR = (L + NT - 1) / NT;  // rows of the table per thread
   // Load the training forward's row terms (BwdArgs::rowtab) instead of
-  // computing them, for 2 rows per thread (16 rows per lane, 128-byte
-  // channel groups): the table's power and division chain then no longer
-  // delays the first sweep row (C2 28.1-28.3 -> 27.3-27.6 us, B=24 N=1024
-  // H=16 27.8 -> 27.5, C4 145.0 either way, gradients bit-identical;
-  // same-box A/B).  With 4 rows per thread (D=32 bf16) the eight loads cost
-  // more than the chain (25.6 -> 26.4 us), with 1 (128-row chunks) the table
-  // is short already (13.5 -> 13.6 us), and with 8 their registers spilled.
-  static constexpr bool kLoadTerms = NR == 2;
+  // computing them, for 1 or 2 rows per thread: the table's power and
+  // division chain then no longer delays the first sweep row (2 rows, 16 per
+  // lane: C2 27.51 -> 27.11-27.28 us, B=24 N=1024 H=16 28.0 -> 27.5, C4
+  // unchanged; 1 row, 128-row chunks: B=8 N=1024 H=6 10.76 -> 10.40, B=2
+  // N=4096 H=12 13.81 -> 13.63, B=8 N=2048 H=12 21.14 -> 21.22; gradients
+  // bit-identical; same-box A/B on shared buffers).  With 4 rows per thread
+  // (D=32 bf16) the eight loads cost more than the chain, and with 8 their
+  // registers spilled.
+  static constexpr bool kLoadTerms = NR <= 2;
   static_assert(G + 1 <= NT, "power table is filled one entry per thread");
 
   // Per row of the chunk (i = the row's index in its lane, 0 <= i < R):
@@ -1270,7 +1271,8 @@ struct ChunkBwd {
     float tx[NR], ty[NR];
 #pragma unroll
     for (int k = 0; k < (kLoadTerms ? NR : 0); ++k) {
-      const int64_t r = row0 + tid + k * NT < a.N ? row0 + tid + k * NT : a.N - 1;
+      const int rr = tid + k * NT < L ? tid + k * NT : L - 1;  // rows of this chunk only
+      const int64_t r = row0 + rr < a.N ? row0 + rr : a.N - 1;
       const float* tp = a.rowtab ? reinterpret_cast<const float*>(a.rowtab + h * a.N + r) : a.lam;
       tx[k] = tp[0];
       ty[k] = (a.rowtab ? tp + 1 : a.lam)[0];
