@@ -1187,8 +1187,9 @@ struct ChunkBwd {
     // groups of 128 bytes or more: for narrower ones the second loop made one
     // of the kernels spill (D=32 bf16, several rounds, 7% slower).  With 16
     // rows, at most two rows' stores in flight per wavefront, as in the
-    // forward (C2 29.65 -> 29.18 us, B=24 N=1024 H=16 29.63 -> 29.29 us,
-    // same-box A/B; no gain with 4 rows).
+    // forward (re-measured on shared buffers, us, none / 1 / 2 / 4 rows in
+    // flight: C2 28.51 / 27.03 / 27.06 / 27.93, B=24 N=1024 H=16 28.80 /
+    // 27.19 / 27.37 / 28.04, C4 145.5 / 146.4 / 145.8 / 145.7).
     if constexpr (LPR >= 8) {
       if (li == R - 1 && (fin_i < 0 || fin_i == R - 1)) {
 #pragma unroll
