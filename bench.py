@@ -138,11 +138,40 @@ def rotated_sets(torch, dev, shape, count: int, seed: int = 1):
     return sets
 
 
-def time_region(torch, launch, steps: int, warmup: int, events: bool = True):
+# Wall time each extra measurement keeps launching before its timed region.
+# After an idle gap (its buffers being allocated and filled) the device runs a
+# memory-bound kernel slower for about 10 ms: back-to-back regions of 100 C2
+# training-forward launches in a fresh process measured 18.7, 19.1, 18.4, 17.9,
+# 17.4, then 17.0-17.1 us per launch, and a backward timed after only 100
+# warm-up launches read 28.6-29.2 us against 26.8-27.2 us once past that ramp
+# (one second of copies or matmuls before the allocation did not remove it).
+EXTRA_WARM_MS = 30.0
+
+
+def warm(torch, launch, ms: float, start: int = 0, batch: int = 64) -> int:
+    """Launch in batches until `ms` of wall time have passed, then synchronise;
+    returns the next launch index."""
+    k, t = start, time.perf_counter()
+    while True:
+        torch.cuda.synchronize()
+        if time.perf_counter() - t >= ms * 1e-3:
+            return k
+        for _ in range(batch):
+            launch(k)
+            k += 1
+
+
+def time_region(torch, launch, steps: int, warmup: int, events: bool = True, warm_ms: float = 0.0):
     """(region ms over `steps` launches, per-launch event durations in ms, or
-    an empty list without `events`)."""
+    an empty list without `events`).
+
+    `warmup` launches first, then, with `warm_ms`, more until that much wall
+    time has passed (the extras; the headline keeps exactly the --warmup count
+    it is given)."""
     for k in range(warmup):
         launch(k)
+    if warm_ms > 0:
+        warm(torch, launch, warm_ms, warmup)
     torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record()
@@ -174,7 +203,7 @@ def copy_bandwidth(torch, dev) -> float:
         a, b = bufs[k % 2]
         b.copy_(a)
 
-    region, _ = time_region(torch, launch, 20, 4)
+    region, _ = time_region(torch, launch, 20, 4, warm_ms=EXTRA_WARM_MS)
     return 2 * n * 2 * 20 / (region * 1e-3) / 1e9
 
 
@@ -197,7 +226,7 @@ def bench_decode(torch, kilat_amd, dev, steps=500):
     def launch(k):
         rc[0] |= lib.kdecay_step(*args)
 
-    region, per = time_region(torch, launch, steps, 20)
+    region, per = time_region(torch, launch, steps, 20, warm_ms=EXTRA_WARM_MS)
     if rc[0]:
         raise RuntimeError("kdecay_step failed")
     us = region * 1e3 / steps
@@ -214,8 +243,7 @@ def bench_decode(torch, kilat_amd, dev, steps=500):
             for _ in range(gsteps):
                 rc[0] |= lib.kdecay_step(*gargs)
     torch.cuda.synchronize()
-    graph.replay()
-    torch.cuda.synchronize()
+    warm(torch, lambda k: graph.replay(), EXTRA_WARM_MS, batch=1)
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record()
     for _ in range(5):
@@ -256,9 +284,7 @@ def bench_decode_layers(torch, kilat_amd, dev, replays=200):
                     kilat_amd.decay_step(lams[l], st[l], v_in[l], tpos, out=outs[l], new_state=st[l])
                 tpos.add_(1)
         torch.cuda.synchronize()
-        for _ in range(10):
-            graph.replay()
-        torch.cuda.synchronize()
+        warm(torch, lambda k: graph.replay(), EXTRA_WARM_MS, batch=1)
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0.record()
         for _ in range(replays):
@@ -280,7 +306,7 @@ def bench_long(torch, kilat_amd, dev, steps=20):
     from kilat_amd import _lib
 
     launch = ScanLauncher(torch, kilat_amd, lam, sets, _lib.KDECAY_BF16)
-    region, per = time_region(torch, launch, steps, 3)
+    region, per = time_region(torch, launch, steps, 3, warm_ms=EXTRA_WARM_MS)
     if launch.rc:
         raise RuntimeError("kdecay_scan_fwd failed")
     nbytes = B * H * N * D * 4
@@ -342,7 +368,7 @@ def bench_forward_dtypes(torch, dev, steps=100):
         def launch(k, args=args, rc=rc):
             rc[0] |= lib.kdecay_scan_fwd(*args[k % len(args)])
 
-        region, _ = time_region(torch, launch, steps, 200, events=False)
+        region, _ = time_region(torch, launch, steps, 200, events=False, warm_ms=EXTRA_WARM_MS)
         if rc[0]:
             raise RuntimeError("scan failed: " + lib.kdecay_last_error_string().decode())
         us = region * 1e3 / steps
@@ -399,8 +425,8 @@ def bench_backward(torch, dev, steps=100):
                                      None, states.data_ptr(), None, dlam.data_ptr(), None, B, H, N, D, 0,
                                      ws.data_ptr(), ws.numel(), stream)
 
-    rf, _ = time_region(torch, fwd, steps, 100, events=False)
-    rb, _ = time_region(torch, bwd, steps, 100, events=False)
+    rf, _ = time_region(torch, fwd, steps, 100, events=False, warm_ms=EXTRA_WARM_MS)
+    rb, _ = time_region(torch, bwd, steps, 100, events=False, warm_ms=EXTRA_WARM_MS)
     if rc[0]:
         raise RuntimeError("training scan failed: " + lib.kdecay_last_error_string().decode())
     fus, bus = rf * 1e3 / steps, rb * 1e3 / steps
@@ -481,8 +507,8 @@ def bench_prefill_cache(torch, dev, model, ids, iters=3):
     layer = {}
     for key, ops, reps in (("reference_seed_loop_us", ReferenceDecayCache(), 3),
                            ("scan_with_final_state_us", KernelDecayCache(), 200)):
-        ops.prefill(kilat_amd.triton_global_decay, lam, V, torch.float32)
-        torch.cuda.synchronize()
+        warm(torch, lambda k: ops.prefill(kilat_amd.triton_global_decay, lam, V, torch.float32), EXTRA_WARM_MS,
+             batch=1)
         t = time.perf_counter()
         for _ in range(reps):
             ops.prefill(kilat_amd.triton_global_decay, lam, V, torch.float32)
@@ -548,8 +574,7 @@ def decay_path_per_layer(torch, dev, reps=200):
         if rc[0]:
             raise RuntimeError("kdecay_scan_fwd failed: " + lib.kdecay_last_error_string().decode())
         torch.cuda.synchronize()
-        g.replay()
-        torch.cuda.synchronize()
+        warm(torch, lambda k: g.replay(), EXTRA_WARM_MS, batch=1)
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0.record()
         for _ in range(3):
