@@ -340,8 +340,10 @@ def measured_traffic(workload: str = "c2"):
 def bench_forward_dtypes(torch, dev, steps=100):
     """The C2 shape (B=8 N=4096 H=12) with other I/O types than the headline's
     bf16: fp16, fp32 in and out (D=64: two 128-byte channel groups per head, so
-    twice the bytes; D=32: C2's bytes), bf16 in / fp32 out, and bf16 with
-    D=128 (twice the bytes).  Algorithmic bytes: V read once, y written once.
+    twice the bytes; D=32: C2's bytes), bf16 in / fp32 out, bf16 with D=128
+    (twice the bytes) and fp64 in and out (D=64: four 128-byte channel groups
+    per head, four times the bytes).  Algorithmic bytes: V read once, y
+    written once.
     4 rotated sets, carved from one allocation as the headline's are (fp16 in
     separate caching-allocator blocks measured 18.2 us against 17.6 us carved,
     the same as bf16 either way)."""
@@ -350,14 +352,16 @@ def bench_forward_dtypes(torch, dev, steps=100):
 
     B, H, N = 8, 12, 4096
     lib = _lib.load()
-    codes = {torch.float32: _lib.KDECAY_F32, torch.bfloat16: _lib.KDECAY_BF16, torch.float16: _lib.KDECAY_F16}
+    codes = {torch.float32: _lib.KDECAY_F32, torch.bfloat16: _lib.KDECAY_BF16, torch.float16: _lib.KDECAY_F16,
+             torch.float64: _lib.KDECAY_F64}
     lam = c2_lam(H, torch).to(dev)
     stream = _stream_ptr(dev)
     out = {}
     for name, ti, to, D in (("f16", torch.float16, torch.float16, 64), ("f32_d64", torch.float32, torch.float32, 64),
                             ("f32_d32", torch.float32, torch.float32, 32),
                             ("bf16_in_f32_out", torch.bfloat16, torch.float32, 64),
-                            ("bf16_d128", torch.bfloat16, torch.bfloat16, 128)):
+                            ("bf16_d128", torch.bfloat16, torch.bfloat16, 128),
+                            ("f64_d64", torch.float64, torch.float64, 64)):
         sets = carved_pairs(torch, dev, (B, H, N, D), ti, to, 4, seed=11)
         nb = lib.kdecay_scan_workspace_bytes(B, H, N, D, codes[ti])
         ws = _workspace(dev, stream, nb)

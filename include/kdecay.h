@@ -38,11 +38,17 @@
 extern "C" {
 #endif
 
-/* Element types of V, y, v_t and the step output. */
+/* Element types of V, y, v_t and the step output.  KDECAY_F64 is taken by
+ * the three forward scans only (kdecay_scan_fwd, kdecay_scan_fwd_noalloc,
+ * kdecay_scan_fwd_sequential), for V and out together; every other entry
+ * point returns KDECAY_EDTYPE for it.  Arithmetic is fp32 for every type, as
+ * in the reference's kernel, which accumulates in fp32 whatever V's dtype
+ * (triton_ops.py:149-152) and stores into out = empty_like(V) (:309). */
 enum {
   KDECAY_F32 = 0,
   KDECAY_BF16 = 1,
-  KDECAY_F16 = 2
+  KDECAY_F16 = 2,
+  KDECAY_F64 = 3
 };
 
 /* Rejected-argument codes (negative). */
@@ -64,7 +70,7 @@ enum {
  *   V            [B,H,N,D] of v_dtype, strides v_strides[4]
  *   out          [B,H,N,D] of out_dtype, strides out_strides[4]
  *                (out_dtype == v_dtype reproduces the reference; F32 out for
- *                 a BF16/F16 V is also accepted)
+ *                 a BF16/F16 V is also accepted; an F64 V takes F64 out only)
  *   init_state   nullable; fp32 [B,H,D] contiguous: state before position 0
  *                (chunked prefill).  NULL means zeros, as the reference.
  *   final_state  nullable; fp32 [B,H,D] contiguous: receives s_{N-1}, the
@@ -96,8 +102,8 @@ enum {
  *                kdecay_scan_workspace_bytes() returns 0.
  *
  * Requirements of this (vector) path: D = 16, 32, or a multiple of 64 (bf16,
- * fp16) or 32 (fp32) channels; d-stride 1; 16-byte aligned V and out; the
- * other strides multiples of 16 bytes.
+ * fp16), 32 (fp32) or 16 (fp64) channels; d-stride 1; 16-byte aligned V and
+ * out; the other strides multiples of 16 bytes.
  * Anything else returns KDECAY_ELAYOUT / KDECAY_ESHAPE without launching.
  */
 int kdecay_scan_fwd(const void* V, int v_dtype, const int64_t* v_strides,

@@ -18,6 +18,7 @@ LIBRARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libkdecay.so
 KDECAY_F32 = 0
 KDECAY_BF16 = 1
 KDECAY_F16 = 2
+KDECAY_F64 = 3  # the three forward scans only
 
 KDECAY_EINVAL = -1
 KDECAY_EDTYPE = -2

@@ -53,6 +53,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(__bf16 x) { return (float)x; }
 __device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(double x) { return (float)x; }
 
 template <typename T>
 __device__ __forceinline__ T from_f32(float x);
@@ -62,6 +63,8 @@ template <>
 __device__ __forceinline__ __bf16 from_f32<__bf16>(float x) { return (__bf16)x; }
 template <>
 __device__ __forceinline__ _Float16 from_f32<_Float16>(float x) { return (_Float16)x; }
+template <>
+__device__ __forceinline__ double from_f32<double>(float x) { return (double)x; }
 
 // 16 bytes of T -> 16/sizeof(T) floats.
 template <typename T>
@@ -96,6 +99,14 @@ __device__ __forceinline__ void unpack16<_Float16>(const uint4& u, float* f) {
   }
 }
 
+// Two doubles, each rounded to float (round to nearest even), as the
+// fp32-arithmetic kernels take every input type.
+template <>
+__device__ __forceinline__ void unpack16<double>(const uint4& u, float* f) {
+  f[0] = (float)__hiloint2double((int)u.y, (int)u.x);
+  f[1] = (float)__hiloint2double((int)u.w, (int)u.z);
+}
+
 __device__ __forceinline__ unsigned pack2(__bf16*, float a, float b) {
   bf16x2 p;
   p.x = (__bf16)a;
@@ -118,7 +129,7 @@ __device__ __forceinline__ void store16_stream(void* p, unsigned a, unsigned b, 
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
 
-// Store N floats (N = 4 or 8) as N elements of T at p (16-byte aligned).
+// Store N floats (N = 4 or 8; 2 for double) as N elements of T at p (16-byte aligned).
 // Eight floats take two 16-byte stores, each of which covers every other 16
 // bytes of the row's range across the lanes: through the cache, whose lines
 // the second store completes before they are written back (non-temporal,
@@ -138,6 +149,11 @@ __device__ __forceinline__ void store_vec(T* p, const float* f) {
     for (int k = 0; k < N / 4; ++k)
       store16_stream(p + 4 * k, __float_as_uint(f[4 * k]), __float_as_uint(f[4 * k + 1]),
                      __float_as_uint(f[4 * k + 2]), __float_as_uint(f[4 * k + 3]));
+  } else if constexpr (sizeof(T) == 8) {
+    static_assert(N == 2, "8-byte outputs are stored 2 at a time");
+    const double d0 = (double)f[0], d1 = (double)f[1];
+    store16_stream(p, (unsigned)__double2loint(d0), (unsigned)__double2hiint(d0), (unsigned)__double2loint(d1),
+                   (unsigned)__double2hiint(d1));
   } else {
     static_assert(N == 8, "2-byte outputs are stored 8 at a time");
     store16_stream(p, pack2((T*)nullptr, f[0], f[1]), pack2((T*)nullptr, f[2], f[3]),
@@ -1748,8 +1764,11 @@ int hip_check(const char* what) {
   return 0;
 }
 
-int elem_size(int dt) { return dt == KDECAY_F32 ? 4 : 2; }
+int elem_size(int dt) { return dt == KDECAY_F32 ? 4 : dt == KDECAY_F64 ? 8 : 2; }
+// Types of the training forward, the backward and the decode step.
 bool dtype_ok(int dt) { return dt == KDECAY_F32 || dt == KDECAY_BF16 || dt == KDECAY_F16; }
+// Types of the three forward scans: also float64 (V and out together).
+bool fwd_dtype_ok(int dt) { return dtype_ok(dt) || dt == KDECAY_F64; }
 
 // Launch shape of the chunked scan: a chunk holds NW * 64 lanes x R rows x
 // 16 bytes = 64 KiB of input whatever the dtype and D, in 64 VGPRs per lane
@@ -1891,6 +1910,25 @@ constexpr int64_t kSixLo = 1280;
 constexpr int64_t kSixLoGroups = 1024;
 constexpr int64_t kSixHi = 1536;
 constexpr int64_t kSixChain = 8;
+// Heads of four or more channel groups (rows of 512 bytes or more, each
+// stream reading every fourth 128-byte slice or sparser) keep the six-per-CU
+// 8-row kernel at any grid of a full round or more, up to 32 chunks per
+// stream: there the 16-row kernel loses 5-16 points.  Measured (same-box A/B
+// on shared buffers, us, 16-row / 8-row six-per-CU, N=4096 unless given):
+// fp64 D=64 B=8 H=12 (3072 chunks) 79.5 / 69.7 (63.3% -> 72.2% of 8 TB/s),
+// B=16 181.9 / 151.5, B=6 58.0 / 53.0; bf16 D=256 B=8 H=12 80.9 / 70.3, fp32
+// D=128 B=8 H=12 80.2 / 70.4; bf16 D=256 H=16: B=2 N=8192 (2048) 62.0 /
+// 47.9, B=4 N=8192 (1024, chains of 16) 101.0 / 94.3, B=2 N=16384 (32 per
+// stream) 97.6 / 91.0, B=8 N=2048 50.3 / 47.4, B=4 H=8 (1024) 29.2 / 25.2;
+// eight groups: fp64 D=128 B=8 H=12 190.5 / 167.0, bf16 D=512 B=8 H=12 192.4
+// / 168.7.  Not below a full round (bf16 D=256 B=2 H=12, 768 chunks: 18.7 /
+// 21.2), not for longer chains (bf16 D=256 B=1 H=16: N=32768, 64 per stream,
+// 96.4 / 117.7; N=65536 189.4 / 231.0), and not for fewer groups (three:
+// bf16 D=192 B=8 H=12 60.7 / 60.4, fp64 D=48 B=12 H=12 89.4 / 90.4; two:
+// fp32 D=64 B=16 H=12 70.1 / 72.4; one: bf16 D=64 B=32 H=12 71.9 / 76.3).
+constexpr int64_t kSixWideGroups = 4;
+constexpr int64_t kSixWideChain = 32;
+constexpr int64_t kSixWideLo = 1024;
 
 // Small grids of few, long streams: 512-row chunks of 8 wavefronts x 8 rows
 // instead of 256-row chunks of 4 wavefronts, which halves the chain a carry
@@ -1920,6 +1958,8 @@ ChunkShape chunk_shape(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) 
   }
   if (full && chain <= kSixChain && grid > (ng > 1 ? kSixLoGroups : kSixLo) && grid <= kSixHi)
     return ChunkShape{kRSmall, kNWSmall, true};
+  if (full && ng >= kSixWideGroups && chain <= kSixWideChain && grid >= kSixWideLo)
+    return ChunkShape{kRSmall, kNWSmall, true};
   return ChunkShape{kR, kNW};
 }
 
@@ -1943,7 +1983,7 @@ int launch_chunked(const ScanArgs& a, int64_t grid, hipStream_t s, bool six = fa
   constexpr bool FZ = R == kRSmall && NW == kNWSmall;
   if constexpr (FZ) {
     if constexpr (LPR == 8) {  // full 128-byte channel groups
-      if (six) {  // chunk_shape's 8-row grid of at most two rounds, six workgroups per CU
+      if (six) {  // chunk_shape's 8-row grid, six workgroups per CU (two rounds at most, except wide heads)
         hipLaunchKernelGGL((scan_chunked<TI, TO, LPR, R, NW, 1, 6, FZ, false>), dim3((unsigned)grid), dim3(NW * 64), 0,
                            s, a);
         return hip_check("scan_chunked launch");
@@ -2012,7 +2052,9 @@ template <typename TI, typename TO, int R, int NW>
 int dispatch_dg_r(const ScanArgs& a, int64_t DG, int64_t grid, hipStream_t s, bool six) {
   switch (DG) {
     case 16: return launch_chunked<TI, TO, 16, R, NW>(a, grid, s, six);
-    case 32: return launch_chunked<TI, TO, 32, R, NW>(a, grid, s, six);
+    case 32:  // a 128-byte group of fp32, or half of one (bf16/fp16); fp64 groups have 16
+      if constexpr (sizeof(TI) <= 4) return launch_chunked<TI, TO, 32, R, NW>(a, grid, s, six);
+      break;
     case 64:
       if constexpr (sizeof(TI) == 2) return launch_chunked<TI, TO, 64, R, NW>(a, grid, s, six);
       break;
@@ -2024,11 +2066,8 @@ template <typename TI, typename TO>
 int dispatch_dg(const ScanArgs& a, int64_t DG, int64_t grid, hipStream_t s, ChunkShape c) {
   if (c.R == kRSmall && c.NW == kNWLong) {
     // Long chains only (window 16, fewer workgroups than twice the CUs: no throttle), full groups.
-    if constexpr (sizeof(TI) == 2) {
-      if (DG == 64) return launch_long<TI, TO, 64>(a, grid, s);
-    } else {
-      if (DG == 32) return launch_long<TI, TO, 32>(a, grid, s);
-    }
+    constexpr int kFull = 128 / (int)sizeof(TI);
+    if (DG == kFull) return launch_long<TI, TO, kFull>(a, grid, s);
     return fail(KDECAY_ESHAPE, "unsupported channel group %lld", (long long)DG);
   }
   if (c.R == kRSmall && c.NW == kNWSmall) return dispatch_dg_r<TI, TO, kRSmall, kNWSmall>(a, DG, grid, s, c.six);
@@ -2162,10 +2201,10 @@ int check_scan_args(const void* V, int v_dtype, const int64_t* v_strides, const 
                     const int64_t* out_strides, const float* lam, int64_t B, int64_t H, int64_t N,
                     int64_t D) {
   if (B < 0 || H < 0 || N < 0 || D < 0) return fail(KDECAY_EINVAL, "negative size");
-  if (!dtype_ok(v_dtype) || !dtype_ok(out_dtype))
+  if (!fwd_dtype_ok(v_dtype) || !fwd_dtype_ok(out_dtype))
     return fail(KDECAY_EDTYPE, "unknown dtype code (v=%d out=%d)", v_dtype, out_dtype);
-  if (out_dtype != v_dtype && out_dtype != KDECAY_F32)
-    return fail(KDECAY_EDTYPE, "out dtype must equal V's dtype or be F32");
+  if (out_dtype != v_dtype && (out_dtype != KDECAY_F32 || v_dtype == KDECAY_F64))
+    return fail(KDECAY_EDTYPE, "out dtype must equal V's dtype or be F32 (F64: V's dtype only)");
   if (B * H * N * D == 0) return 0;
   if (!V || !out || !lam || !v_strides || !out_strides) return fail(KDECAY_EINVAL, "null pointer argument");
   return 0;
@@ -2241,7 +2280,7 @@ uint32_t kdecay_debug_fastdiv(uint32_t n, uint32_t d, int want_mod) {
 }
 
 size_t kdecay_scan_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
-  if (B <= 0 || H <= 0 || N <= 0 || !dtype_ok(v_dtype) || !head_dim_ok(v_dtype, D)) return 0;
+  if (B <= 0 || H <= 0 || N <= 0 || !fwd_dtype_ok(v_dtype) || !head_dim_ok(v_dtype, D)) return 0;
   const int64_t L = chunk_rows(v_dtype, D, chunk_shape(B, H, N, D, v_dtype));
   const int64_t nchunk = (N + L - 1) / L;
   if (nchunk <= 1) return 0;
@@ -2315,6 +2354,7 @@ static int scan_fwd_impl(const void* V, int v_dtype, const int64_t* v_strides, v
   a.rowtab = a.states ? reinterpret_cast<float2*>(states + B * H * D * a.nsaved) : nullptr;
 
   if (v_dtype == KDECAY_F32) return dispatch_dg<float, float>(a, DG, grid, s, shape);
+  if (v_dtype == KDECAY_F64) return dispatch_dg<double, double>(a, DG, grid, s, shape);
   if (v_dtype == KDECAY_BF16) {
     if (out_dtype == KDECAY_BF16) return dispatch_dg<__bf16, __bf16>(a, DG, grid, s, shape);
     return dispatch_dg<__bf16, float>(a, DG, grid, s, shape);
@@ -2367,6 +2407,9 @@ int kdecay_scan_fwd_train(const void* V, int v_dtype, const int64_t* v_strides, 
                           float* final_state, float* states, size_t states_floats, int64_t B, int64_t H,
                           int64_t N, int64_t D, int64_t t_offset, void* workspace, size_t workspace_bytes,
                           void* stream) {
+  // The backward that reads these states takes no float64 (dtype_ok).
+  if (!dtype_ok(v_dtype) || !dtype_ok(out_dtype))
+    return fail(KDECAY_EDTYPE, "training forward: dtype code (v=%d out=%d) not F32/BF16/F16", v_dtype, out_dtype);
   const size_t need = kdecay_scan_saved_states_floats(B, H, N, D, v_dtype);
   if (need && (!states || states_floats < need))
     return fail(KDECAY_EINVAL, "states buffer of %zu floats required, %zu given", need, states_floats);
@@ -2521,6 +2564,7 @@ int kdecay_scan_fwd_sequential(const void* V, int v_dtype, const int64_t* v_stri
   a.D = D;
   a.t_offset = t_offset;
   if (v_dtype == KDECAY_F32) return launch_seq<float, float>(a, s);
+  if (v_dtype == KDECAY_F64) return launch_seq<double, double>(a, s);
   if (v_dtype == KDECAY_BF16) {
     if (out_dtype == KDECAY_BF16) return launch_seq<__bf16, __bf16>(a, s);
     return launch_seq<__bf16, float>(a, s);

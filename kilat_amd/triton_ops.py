@@ -28,16 +28,17 @@ _DTYPE_CODE = {
     torch.float32: _lib.KDECAY_F32,
     torch.bfloat16: _lib.KDECAY_BF16,
     torch.float16: _lib.KDECAY_F16,
+    torch.float64: _lib.KDECAY_F64,
 }
 
 
 # Channels of one full 128-byte channel group, per element type.
-_GROUP = {torch.float32: 32, torch.bfloat16: 64, torch.float16: 64}
+_GROUP = {torch.float32: 32, torch.bfloat16: 64, torch.float16: 64, torch.float64: 16}
 
 
 def chunked_head_dim(D: int, dtype: torch.dtype) -> bool:
     """Head dims the chunked kernels take as they are: 16, 32, or a multiple of
-    one 128-byte channel group (64 bf16/fp16 or 32 fp32 channels).  Other head
+    one 128-byte channel group (64 bf16/fp16, 32 fp32 or 16 fp64 channels).  Other head
     dims are zero-padded to the next such size on the way in (channels are
     independent, so the padding changes no value) and sliced on the way out."""
     return D == 16 or D == 32 or (D > 0 and D % _GROUP[dtype] == 0)
@@ -74,7 +75,7 @@ def _dtype_code(t: torch.Tensor, name: str) -> int:
     try:
         return _DTYPE_CODE[t.dtype]
     except KeyError:
-        raise TypeError(f"kilat_amd: {name} dtype {t.dtype} is not float32/bfloat16/float16") from None
+        raise TypeError(f"kilat_amd: {name} dtype {t.dtype} is not float32/bfloat16/float16/float64") from None
 
 
 def _vector_layout_ok(t: torch.Tensor) -> bool:
@@ -177,7 +178,10 @@ def reserve_workspace(
     lib = _lib.load()
     nbytes = lib.kdecay_scan_workspace_bytes(B, H, N, D, code)
     if backward:
-        nbytes = max(nbytes, lib.kdecay_scan_bwd_workspace_bytes(B, H, N, D, code))
+        # float64 is trained through the fp32 kernels (_scan_with_grad)
+        tcode = _lib.KDECAY_F32 if code == _lib.KDECAY_F64 else code
+        nbytes = max(nbytes, lib.kdecay_scan_workspace_bytes(B, H, N, D, tcode),
+                     lib.kdecay_scan_bwd_workspace_bytes(B, H, N, D, tcode))
     with _on_device(dev):
         ws = _workspace(dev, _stream_ptr(dev), nbytes)
     return 0 if ws is None else ws.numel()
@@ -321,8 +325,9 @@ def global_decay_scan(
 ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
     """y[b,h,t] = s[b,h,t] / z_t with s_t = lam_h * s_{t-1} + V[b,h,t].
 
-    lam: [H] (any float dtype; used as fp32).  V: [B,H,N,D] fp32/bf16/fp16, any
-    strides.  initial_state: [B,H,D] state before position 0 (default zeros).
+    lam: [H] (any float dtype; used as fp32).  V: [B,H,N,D] fp32/bf16/fp16/fp64,
+    any strides (arithmetic in fp32 for every type, as the reference's kernel
+    accumulates).  initial_state: [B,H,D] state before position 0 (default zeros).
     t_offset: absolute position of row 0 (z uses t_offset + t).
     Returns y ([B,H,N,D], dtype out_dtype or V.dtype, laid out like V), and
     with return_final_state also s_{N-1} ([B,H,D] fp32).
@@ -333,7 +338,8 @@ def global_decay_scan(
     algorithm and out= (the gradients always come from the chunked backward
     kernel).  The backward kernel takes the upstream gradient in V's dtype:
     with out_dtype=float32 for a bf16/fp16 V, that gradient is rounded to V's
-    dtype first.
+    dtype first.  A float64 V takes float64 out only; with a gradient it runs
+    the fp32 training kernels on V rounded to fp32.
     """
     _require_hip(V, "V")
     if V.dim() != 4:
@@ -351,8 +357,8 @@ def global_decay_scan(
         if out.shape != V.shape or out.device != dev:
             raise ValueError("kilat_amd: out must have V's shape and device")
     o_code = _dtype_code(out, "out")
-    if o_code != v_code and o_code != _lib.KDECAY_F32:
-        raise TypeError("kilat_amd: out dtype must be V's dtype or float32")
+    if o_code != v_code and (o_code != _lib.KDECAY_F32 or v_code == _lib.KDECAY_F64):
+        raise TypeError("kilat_amd: out dtype must be V's dtype or float32 (V's dtype for a float64 V)")
     init32 = None
     if initial_state is not None:
         _require_hip(initial_state, "initial_state")
@@ -434,6 +440,16 @@ def _scan_with_grad(lam, V, initial_state, return_final_state, t_offset, out, ou
         y, final = _scan_with_grad(lam, V, initial_state, True, t_offset, None, out.dtype, algorithm)
         out.copy_(y)
         return (out, final) if return_final_state else out
+    if V.dtype == torch.float64:
+        # The training forward and backward kernels take fp32/bf16/fp16 only.  A
+        # float64 V runs them on V rounded to fp32 (the rounding the forward
+        # kernels apply to each float64 element as they load it) and y comes
+        # back as float64; dV reaches V through the rounding's own gradient.
+        if (out_dtype or V.dtype) != torch.float64:
+            raise TypeError("kilat_amd: out dtype must be V's dtype for a float64 V")
+        y, final = _scan_with_grad(lam, V.float(), initial_state, True, t_offset, None, torch.float32, algorithm)
+        y = y.to(torch.float64)
+        return (y, final) if return_final_state else y
     if not chunked_head_dim(D, V.dtype):
         Dp = _padded_head_dim(D, V.dtype)
         Vp = torch.nn.functional.pad(V, (0, Dp - D))
@@ -497,7 +513,8 @@ def decay_step(
         out       = new_state / ((1 - lam**(t_pos+1)) / (1 - lam + 1e-6))
 
     past_state: [B,H,D] (used as fp32, as the reference's promotion makes it).
-    v_t: [B,H,D] fp32/bf16/fp16 (any view of [B,1,H*D] reshapes to it).
+    v_t: [B,H,D] fp32/bf16/fp16/fp64 (any view of [B,1,H*D] reshapes to it;
+    fp64 is rounded to fp32 first, out_dtype float64 widens the fp32 result).
     t_pos: int shared by the batch (the reference's cache length) or an int
     tensor [B] of per-sequence positions.  new_state may be past_state itself
     (in-place).  Returns (out [B,H,D] out_dtype, new_state [B,H,D] fp32).
@@ -512,6 +529,8 @@ def decay_step(
         raise ValueError(f"kilat_amd: v_t has {v_t.numel()} elements, expected B*H*D={B * H * D}")
     v_code = _dtype_code(v_t, "v_t")
     vk = v_t.detach().reshape(B, H, D).contiguous()
+    if v_code == _lib.KDECAY_F64:  # the step kernel takes v_t as fp32 (rounded once), as every type
+        vk, v_code = vk.float(), _lib.KDECAY_F32
     lam32 = _lam32(lam, H, dev)
     s_in = past_state.detach()
     if s_in.dtype != torch.float32 or not s_in.is_contiguous():
@@ -525,6 +544,9 @@ def decay_step(
     elif not out.is_contiguous() or out.numel() != B * H * D:
         raise ValueError("kilat_amd: out must be contiguous with B*H*D elements")
     o_code = _dtype_code(out, "out")
+    outk = out
+    if o_code == _lib.KDECAY_F64:  # computed in fp32, then widened exactly
+        outk, o_code = torch.empty((B, H, D), dtype=torch.float32, device=dev), _lib.KDECAY_F32
     tpos_ptr, tpos_scalar, tpos_dev = None, 0, None
     if isinstance(t_pos, torch.Tensor):
         if t_pos.numel() != B:
@@ -537,10 +559,12 @@ def decay_step(
     with _on_device(dev):
         rc = lib.kdecay_step(
             lam32.data_ptr(), s_in.data_ptr(), vk.data_ptr(), v_code,
-            new_state.data_ptr(), out.data_ptr(), o_code,
+            new_state.data_ptr(), outk.data_ptr(), o_code,
             tpos_ptr, tpos_scalar, B, H, D, _stream_ptr(dev),
         )
     _lib.check(rc, "kdecay_step")
+    if outk is not out:
+        out.copy_(outk.reshape(out.shape))
     return out, new_state
 
 

@@ -12,7 +12,7 @@ _kd.kdecay_scan_fwd.argtypes = [_P, _I, _P, _P, _I, _P, _P, _P, _P, _I64, _I64, 
 _kd.kdecay_scan_workspace_bytes.restype = ctypes.c_size_t
 _kd.kdecay_scan_workspace_bytes.argtypes = [_I64, _I64, _I64, _I64, _I]
 _kd.kdecay_last_error_string.restype = ctypes.c_char_p
-_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2, torch.float64: 3}
 _WS = {}    # one zeroed workspace per (device, stream)
 _KEEP = []  # replaced workspaces: a captured graph may still use one, so none is ever freed
 

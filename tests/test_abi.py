@@ -58,6 +58,19 @@ def test_workspace_bytes(kdecay_lib):
     assert ws(1, 16, 65536, 128, _lib.KDECAY_BF16) == 256 + 16 * 128 * 128 * 8  # 4096 chunks
     assert ws(2, 6, 512, 64, _lib.KDECAY_BF16) == 256 + 2 * 6 * 2 * 64 * 8  # small grid: 256-row chunks
     assert ws(2, 6, 256, 64, _lib.KDECAY_BF16) == 0  # one chunk per stream
+    # float64: 16-channel groups, 8 lanes per row as fp32's 32-channel groups, so
+    # D fp64 channels make the streams and chunks of 2D fp32 channels, with half
+    # the channels' words
+    for B, H, N, D in ((8, 12, 4096, 64), (2, 6, 512, 16), (1, 16, 65536, 128), (2, 3, 3000, 48)):
+        assert ws(B, H, N, D, _lib.KDECAY_F64) - 256 == (ws(B, H, N, 2 * D, _lib.KDECAY_F32) - 256) // 2 > 0
+    assert ws(2, 6, 128, 16, _lib.KDECAY_F64) == 0  # one chunk per stream
+    # heads of four or more 128-byte groups, a full round of 512-row chunks or more and at
+    # most 32 per stream: 256-row chunks (the six-per-CU kernel)
+    assert ws(8, 12, 4096, 256, _lib.KDECAY_BF16) == 256 + 8 * 12 * 16 * 256 * 8  # 3072 chunks at 512 rows
+    assert ws(2, 16, 16384, 256, _lib.KDECAY_BF16) == 256 + 2 * 16 * 64 * 256 * 8  # 32 per stream
+    assert ws(1, 16, 32768, 256, _lib.KDECAY_BF16) == 256 + 16 * 64 * 256 * 8  # 64 per stream: 512 rows
+    assert ws(2, 12, 4096, 256, _lib.KDECAY_BF16) == 256 + 2 * 12 * 8 * 256 * 8  # 768 chunks: 512 rows
+    assert ws(8, 12, 4096, 192, _lib.KDECAY_BF16) == 256 + 8 * 12 * 8 * 192 * 8  # three groups: 512 rows
     assert ws(2, 6, 1024, 64, _lib.KDECAY_F32) == 256 + 2 * 6 * 4 * 64 * 8  # 2 groups of 32, 256-row chunks
     assert ws(1, 2, 4096, 32, _lib.KDECAY_BF16) == 256 + 2 * 8 * 32 * 8  # 32-channel rows: 512-row chunks
     assert ws(8, 12, 2048, 64, _lib.KDECAY_BF16) == 256 + 8 * 12 * 8 * 64 * 8  # 384 chunks at 16 rows: 8
@@ -133,6 +146,7 @@ def test_saved_states_floats(kdecay_lib):
     assert sf(8, 12, 4096, 128, _lib.KDECAY_BF16) == 8 * 12 * 128 * (4096 // 256) + 2 * 12 * 4096  # whole rows
     assert sf(2, 6, 100, 64, _lib.KDECAY_BF16) == 0  # one chunk per stream
     assert sf(2, 6, 4096, 48, _lib.KDECAY_BF16) == 0  # unsupported D
+    assert sf(8, 12, 4096, 64, _lib.KDECAY_F64) == 0  # no float64 training kernels
 
 
 def _scan(lib, v_dtype=_lib.KDECAY_BF16, out_dtype=None, D=64, N=4096, vstr=None, ostr=None,
@@ -149,6 +163,10 @@ def test_scan_rejects_bad_arguments(kdecay_lib):
     lib = kdecay_lib
     assert _scan(lib, v_dtype=7) == _lib.KDECAY_EDTYPE
     assert _scan(lib, v_dtype=_lib.KDECAY_BF16, out_dtype=_lib.KDECAY_F16) == _lib.KDECAY_EDTYPE
+    assert _scan(lib, v_dtype=_lib.KDECAY_F64, out_dtype=_lib.KDECAY_F32) == _lib.KDECAY_EDTYPE
+    assert _scan(lib, v_dtype=_lib.KDECAY_F32, out_dtype=_lib.KDECAY_F64) == _lib.KDECAY_EDTYPE
+    assert _scan(lib, v_dtype=_lib.KDECAY_F64, D=24) == _lib.KDECAY_ESHAPE
+    assert _scan(lib, v_dtype=_lib.KDECAY_F64, D=48) == _lib.KDECAY_EWORKSPACE  # a float64 head dim
     assert _scan(lib, D=48) == _lib.KDECAY_ESHAPE
     assert _scan(lib, V=FAKE + 2) == _lib.KDECAY_ELAYOUT
     assert _scan(lib, vstr=(3 * 4096 * 64, 4096 * 64, 64, 2)) == _lib.KDECAY_ELAYOUT
@@ -271,6 +289,16 @@ def test_sequential_and_step_reject_bad_arguments(kdecay_lib):
     assert lib.kdecay_scan_fwd_sequential(FAKE, 0, s4, FAKE, 0, s4, FAKE, None, None, 1, 1, 1, 2048, 0,
                                           None) == _lib.KDECAY_ESHAPE
     assert lib.kdecay_step(FAKE, FAKE, FAKE, 5, FAKE, FAKE, 0, None, 0, 1, 1, 1, None) == _lib.KDECAY_EDTYPE
+    # float64 is taken by the three forward scans only
+    f64 = _lib.KDECAY_F64
+    assert lib.kdecay_step(FAKE, FAKE, FAKE, f64, FAKE, FAKE, 0, None, 0, 1, 1, 4, None) == _lib.KDECAY_EDTYPE
+    assert lib.kdecay_step(FAKE, FAKE, FAKE, 0, FAKE, FAKE, f64, None, 0, 1, 1, 4, None) == _lib.KDECAY_EDTYPE
+    st = _lib.strides4((3 * 4096 * 64, 4096 * 64, 64, 1))
+    assert lib.kdecay_scan_fwd_train(FAKE, f64, st, FAKE, f64, st, FAKE, None, None, FAKE, 1 << 30, 2, 3, 4096, 64,
+                                     0, FAKE, 1 << 30, None) == _lib.KDECAY_EDTYPE
+    assert lib.kdecay_scan_bwd_workspace_bytes(8, 12, 4096, 64, f64) == 0
+    assert lib.kdecay_scan_fwd_sequential(FAKE, f64, s4, FAKE, 0, s4, FAKE, None, None, 1, 1, 1, 16, 0,
+                                          None) == _lib.KDECAY_EDTYPE  # out must be float64 too
     assert lib.kdecay_step(None, FAKE, FAKE, 0, FAKE, FAKE, 0, None, 0, 1, 1, 1, None) == _lib.KDECAY_EINVAL
     assert lib.kdecay_step(FAKE, FAKE, FAKE, 0, FAKE, FAKE, 0, None, 0, -1, 1, 1, None) == _lib.KDECAY_EINVAL
     # empty problems are valid no-ops
@@ -384,7 +412,7 @@ def test_chunked_head_dims_and_padding():
 
     from kilat_amd.triton_ops import _padded_head_dim, chunked_head_dim
 
-    for dt, full in ((torch.bfloat16, 64), (torch.float16, 64), (torch.float32, 32)):
+    for dt, full in ((torch.bfloat16, 64), (torch.float16, 64), (torch.float32, 32), (torch.float64, 16)):
         for D in (16, 32, full, 2 * full, 3 * full, 8 * full):
             assert chunked_head_dim(D, dt), (dt, D)
             assert _padded_head_dim(D, dt) == D
@@ -401,7 +429,8 @@ def test_library_takes_the_same_head_dims(kdecay_lib):
 
     from kilat_amd.triton_ops import chunked_head_dim
 
-    for dt, code in ((torch.bfloat16, _lib.KDECAY_BF16), (torch.float32, _lib.KDECAY_F32)):
+    for dt, code in ((torch.bfloat16, _lib.KDECAY_BF16), (torch.float32, _lib.KDECAY_F32),
+                     (torch.float64, _lib.KDECAY_F64)):
         for D in range(1, 400):
             ok = kdecay_lib.kdecay_scan_workspace_bytes(2, 3, 100000, D, code) > 0
             assert ok == chunked_head_dim(D, dt), (dt, D)

@@ -544,3 +544,29 @@ def test_backward_layout_fused_and_broadcast_gradient(hip_device, kdecay_lib, B,
     rdv, rdl, _ = O.scan_grads_f64(lam, V, torch.ones(B, H, N, D, dtype=torch.float64))
     dv = P.grad.cpu().view(B, N, H, D).transpose(1, 2)
     check(dv, lam_d.grad.cpu(), None, rdv, rdl, None, torch.bfloat16, f"fused layout B={B} N={N}")
+
+
+def test_backward_float64_runs_the_fp32_kernels(hip_device, kdecay_lib):
+    """A float64 V with a gradient runs the fp32 training forward and backward
+    on V rounded to fp32: y, dV and dlam equal those of the same call on
+    V.float() (widened to float64 where V's type is float64), and are within
+    the fp32 bounds of the oracle's float64 gradients."""
+    g = torch.Generator().manual_seed(650)
+    B, H, N, D = 2, 3, 1500, 64
+    dev = hip_device
+    lam = lam_uniform(H, 0.6, 0.999, g)
+    V = torch.randn(B, H, N, D, generator=g, dtype=torch.float64)
+    gy = torch.randn(B, H, N, D, generator=g, dtype=torch.float64)
+    Vd, ld = V.to(dev).requires_grad_(True), lam.to(dev).requires_grad_(True)
+    y = kilat_amd.triton_global_decay(ld, Vd)
+    assert y.dtype == torch.float64
+    (y * gy.to(dev)).sum().backward()
+    V32, l32 = V.float().to(dev).requires_grad_(True), lam.to(dev).requires_grad_(True)
+    y32 = kilat_amd.triton_global_decay(l32, V32)
+    (y32 * gy.float().to(dev)).sum().backward()
+    torch.cuda.synchronize()
+    assert Vd.grad.dtype == torch.float64
+    assert torch.equal(y, y32.double()) and torch.equal(Vd.grad, V32.grad.double()) and torch.equal(ld.grad, l32.grad)
+    rdv, rdl, _ = oracle_grads(lam, V, gy)
+    assert rel_err(Vd.grad.cpu(), rdv) <= 1e-5
+    assert rel(ld.grad.cpu(), rdl) <= 1e-4

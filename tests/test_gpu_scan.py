@@ -680,3 +680,101 @@ def test_small_grid_throttled_stores(hip_device, kdecay_lib, dname, out, B, H, N
         ref, sref = O.scan(lam, V, out_dtype=out)
         assert_parity(y, ref, out or dtype, f"{dname} N={n}")
         assert rel_err(fin, sref) <= 1e-5
+
+
+# ---------------------------------------------------------------------------
+# float64 V.  The reference's kernel takes any floating dtype, accumulates in
+# fp32 and stores into out = empty_like(V) (triton_ops.py:149-152, 309); the
+# float64 launch loads each element rounded to fp32 once, computes as the fp32
+# kernels do and widens each output exactly.
+# ---------------------------------------------------------------------------
+def _embed_f64_groups(V64):
+    """V64 rounded to fp32, each 16-channel group of the float64 head in the
+    first half of a 32-channel fp32 group (zeros in the second): an fp32 launch
+    with the same streams, chunks and lanes per row as the float64 one."""
+    B, H, N, D = V64.shape
+    V32 = torch.zeros(B, H, N, D // 16, 32, dtype=torch.float32, device=V64.device)
+    V32[..., :16] = V64.float().reshape(B, H, N, D // 16, 16)
+    return V32.reshape(B, H, N, 2 * D)
+
+
+def _f64_channels(y32, D):
+    B, H, N, _ = y32.shape
+    return y32.reshape(B, H, N, D // 16, 32)[..., :16].reshape(B, H, N, D)
+
+
+@pytest.mark.parametrize("B,H,N,D", [(2, 3, 3000, 16), (1, 4, 20000, 16), (2, 3, 1000, 64), (8, 12, 1100, 64),
+                                     (4, 16, 2048, 48), (8, 12, 4096, 64)])
+def test_scan_f64_is_the_fp32_kernel_on_rounded_input(hip_device, kdecay_lib, B, H, N, D):
+    """Small grids (8 rows per lane, and the long-chain 8-wavefront kernel at
+    N=20000), large grids and a 3-group head: the float64 output equals the
+    fp32 kernel's on the embedded rounded input, widened, bit for bit (the
+    look-back folds from the start of each stream, so equal geometry gives
+    equal bits); the final states too; and y is within the fp32 bound of the
+    oracle's float64 path (the reference's CPU loop in V's dtype)."""
+    g = torch.Generator().manual_seed(600 + D + N)
+    lam = lam_uniform(H, 0.5, 0.9999, g)
+    V = torch.randn(B, H, N, D, generator=g, dtype=torch.float64)
+    y, fin = gpu_scan(lam, V, hip_device, return_final_state=True)
+    assert y.dtype == torch.float64 and y.shape == V.shape
+    y32, fin32 = gpu_scan(lam, _embed_f64_groups(V.to(hip_device)), hip_device, return_final_state=True)
+    assert torch.equal(y, _f64_channels(y32, D).double())
+    assert torch.equal(fin, _f64_channels(fin32.unsqueeze(2), D).squeeze(2))
+    ref, sref = O.scan(lam, V)
+    assert ref.dtype == torch.float64
+    e = rel_err(y, ref)
+    assert e <= 1e-5, f"float64 rel_err {e:.3e}"
+    assert rel_err(fin, sref) <= 1e-5
+
+
+def test_scan_f64_carry_offset_layout_and_sequential(hip_device, kdecay_lib):
+    """float64 V in the projection layout ((B,N,H*D) viewed as (B,H,N,D)), with
+    a carried-in state and a position offset: equal bits to the same V made
+    contiguous, within the fp32 bound of the oracle; the sequential kernel on
+    float64 equals the sequential kernel on V rounded to fp32, widened."""
+    g = torch.Generator().manual_seed(611)
+    B, H, N, D = 3, 4, 2500, 32
+    lam = lam_uniform(H, 0.5, 0.9999, g)
+    flat = torch.randn(B, N, H * D, generator=g, dtype=torch.float64)
+    init = torch.randn(B, H, D, generator=g)
+    dev = hip_device
+    V = flat.to(dev).view(B, N, H, D).transpose(1, 2)
+    assert not V.is_contiguous()
+    kw = dict(initial_state=init.to(dev), t_offset=77, return_final_state=True)
+    y, fin = gpu_scan(lam, V, dev, **kw)
+    yc, finc = gpu_scan(lam, V.contiguous(), dev, **kw)
+    assert y.dtype == torch.float64 and torch.equal(y, yc) and torch.equal(fin, finc)
+    ref, sref = O.scan(lam, V.cpu(), init_state=init, t_offset=77)
+    assert rel_err(y, ref) <= 1e-5 and rel_err(fin, sref) <= 1e-5
+    ys, fins = gpu_scan(lam, V, dev, algorithm="sequential", **kw)
+    ys32, fins32 = gpu_scan(lam, V.float(), dev, algorithm="sequential", **kw)
+    assert ys.dtype == torch.float64 and torch.equal(ys, ys32.double()) and torch.equal(fins, fins32)
+    assert rel_err(ys, ref) <= 1e-5
+
+
+def test_scan_f64_rejects_float32_out_and_pads_other_head_dims(hip_device, kdecay_lib):
+    """A float64 V writes float64 only (as empty_like(V)); head dims that are
+    not a multiple of 16 are zero-padded like any other type's."""
+    g = torch.Generator().manual_seed(612)
+    lam = lam_uniform(2, 0.6, 0.999, g)
+    V = torch.randn(1, 2, 700, 24, generator=g, dtype=torch.float64)
+    with pytest.raises(TypeError, match="float64"):
+        kilat_amd.global_decay_scan(lam.to(hip_device), V.to(hip_device), out_dtype=torch.float32)
+    y = gpu_scan(lam, V, hip_device)
+    assert y.dtype == torch.float64 and y.shape == V.shape
+    assert rel_err(y, O.scan(lam, V)[0]) <= 1e-5
+
+
+@pytest.mark.parametrize("B,H,N,D,dname", [(2, 16, 8192, 256, "bf16"), (8, 12, 4096, 128, "f32")])
+def test_scan_wide_heads_several_rounds(hip_device, kdecay_lib, B, H, N, D, dname):
+    """Heads of four 128-byte channel groups on grids of several rounds: the
+    six-per-CU 8-row kernel in 2.7 and 4 rounds (4096 and 6144 chunks of 256
+    rows), against the oracle."""
+    dtype = DTYPES[dname]
+    g = torch.Generator().manual_seed(660 + D)
+    lam = lam_uniform(H, 0.5, 0.9999, g)
+    V = torch.randn(B, H, N, D, generator=g).to(dtype)
+    y, fin = gpu_scan(lam, V, hip_device, return_final_state=True)
+    ref, sref = O.scan(lam, V)
+    assert_parity(y, ref, dtype, f"{dname} D={D}")
+    assert rel_err(fin, sref) <= 1e-5

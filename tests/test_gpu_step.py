@@ -392,3 +392,26 @@ def test_decode_token_all_layers_in_one_graph(hip_device, kdecay_lib, B):
             assert torch.equal(st_d[l].cpu(), ref_states[l]), (t, l)
             assert ulps(outs[l], ro).max() <= 1, (t, l)
     assert torch.equal(tpos.cpu(), tpos0 + T)
+
+
+def test_step_float64_v_and_out(hip_device, kdecay_lib):
+    """float64 v_t is rounded to fp32 once (the state is fp32, as for every
+    type) and a float64 out holds the fp32 result widened: equal bits to the
+    same step on v_t rounded to fp32; within fp32 rounding of the oracle's
+    step in float64."""
+    g = torch.Generator().manual_seed(640)
+    lam = lam_uniform(6, 0.5, 0.9999, g)
+    dev = hip_device
+    state = torch.randn(8, 6, 64, generator=g) * 4
+    v = torch.randn(8, 6, 64, generator=g, dtype=torch.float64)
+    for tp in (0, 5, 4095):
+        print(f"  step float64 t_pos={tp}", flush=True)
+        out, ns = kilat_amd.decay_step(lam.to(dev), state.to(dev), v.to(dev), tp, out_dtype=torch.float64)
+        out32, ns32 = kilat_amd.decay_step(lam.to(dev), state.to(dev), v.float().to(dev), tp)
+        torch.cuda.synchronize()
+        assert out.dtype == torch.float64 and ns.dtype == torch.float32
+        assert torch.equal(ns, ns32) and torch.equal(out, out32.double())
+        ro, rs = O.step(lam, state, v, tp)
+        assert ro.dtype == torch.float64
+        assert float((out.cpu() - ro).abs().max() / ro.abs().max()) <= 1e-6
+        assert float((ns.cpu().double() - rs).abs().max() / rs.abs().max()) <= 1e-6
