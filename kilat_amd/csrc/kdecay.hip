@@ -2103,6 +2103,24 @@ constexpr int64_t kBwdShortChainGrid = 384;
 // N=4096 H=12 (384, 8) 22.9 / 22.2; B=2 N=8192 H=12 (384, 16) 31.7 / 22.3;
 // B=8 N=2048 H=14 (448, 4) 23.2 / 22.9; D=32 B=8 N=4096 H=12 (384, 4)
 // 24.5 / 28.6; D=32 B=8 N=4096 H=16 (512, 4) 32.4 / 29.8.
+// 8 rows per lane (256-row chunks, 128 VGPRs, four workgroups per CU
+// instead of three) for heads of two or more 128-byte channel groups, when
+// the 16-row grid runs more than one round and has at least 48 streams.
+// Measured (same-box A/B on shared buffers, each variant's own saved states,
+// us, 16 / 8 rows; N=4096 H=12 unless given): fp32 D=64 B=5 (960 chunks of
+// 512 rows) 42.4 / 39.4, B=6 50.9 / 46.9, B=8 (two rounds) 64.7 / 60.1, B=16
+// 109.6 / 106.8; fp32 D=128 B=4 66.8 / 59.0, B=8 113.4 / 102.5; fp32 D=64
+// H=16 B=2 N=16384 78.3 / 74.4, B=24 N=1024 58.4 / 57.4; fp32 D=128 B=1 H=16
+// N=65536 (64 streams) 280.6 / 263.9 (71.8% -> 76.3% of 8 TB/s); bf16 D=128
+// B=2 H=16 N=32768 (64 streams) 146.0 / 140.9, bf16 D=256 B=1 N=65536 (48)
+// 217.1 / 208.2.  Not in one round (fp32 D=64 B=4, 768 chunks: 30.1 /
+// 33.7), not for one-group heads (fp32 D=32 B=12 H=12 46.8 / 48.6, bf16 D=64
+// B=16 H=12 60.8 / 62.5, C2 27.2 / 35.6) and not for fewer streams (bf16
+// D=128 B=1 H=16 N=65536, 32 streams: 145.7 / 147.5; fp16 147.0 / 147.9).
+// Whole 256-byte rows keep 16 rows (bwd_group_width).
+constexpr int kRBMid = 8;
+constexpr int64_t kBwdOneRound = 768;  // resident 16-row chunks on 256 CUs
+constexpr int64_t kBwdMidStreams = 48;
 int bwd_rows_per_lane(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   const int64_t vw = 16 / elem_size(v_dtype);
   const int64_t DG = bwd_group_width(B, H, N, D, v_dtype);
@@ -2110,7 +2128,10 @@ int bwd_rows_per_lane(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   const int64_t nstream = B * H * (D / DG);
   const int64_t chain = (N + L - 1) / L;
   const int64_t grid = chain * nstream;
-  return grid <= kBwdSmallGrid || (grid <= kBwdShortChainGrid && chain <= 4) ? kRBSmall : kRB;
+  if (grid <= kBwdSmallGrid || (grid <= kBwdShortChainGrid && chain <= 4)) return kRBSmall;
+  if (DG * elem_size(v_dtype) == 128 && D / DG >= 2 && grid > kBwdOneRound && nstream >= kBwdMidStreams)
+    return kRBMid;
+  return kRB;
 }
 
 int64_t bwd_chunk_rows(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
@@ -2134,6 +2155,14 @@ int launch_bwd(const BwdArgs& a, int64_t grid, int R, hipStream_t s) {
                     : a.nchunk > 8                  ? scan_bwd<T, LPR, kRB, kNWB, 8, 3>
                                                     : one_round;
     hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(kNWB * 64), 0, s, a);
+  } else if (R == kRBMid) {
+    // Several rounds of 256-row chunks (bwd_rows_per_lane): more chunks than
+    // the 1024 resident at four workgroups per CU, so the several-round window.
+    if constexpr (LPR == 8) {
+      hipLaunchKernelGGL((scan_bwd<T, LPR, kRBMid, kNWB, kWRounds, 4>), dim3((unsigned)grid), dim3(kNWB * 64), 0, s, a);
+    } else {
+      return fail(KDECAY_ESHAPE, "no 8-row backward kernel for %d-channel groups", DG);
+    }
   } else if constexpr (LPR >= 16) {
     // Whole 256-byte rows only on large grids (bwd_group_width), which take
     // 16 rows per lane.

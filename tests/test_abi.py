@@ -133,6 +133,18 @@ def test_backward_workspace_bytes(kdecay_lib):
     nst, nch = 4 * 6 * 2, 4096 // 512
     assert wb(4, 6, 4096, 128, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
 
+    def words(B, H, N, D, nst, nch):
+        return 256 + B * H * nch * D * 8 + (nst * nch * 8 + 255) // 256 * 256
+
+    # heads of two or more 128-byte groups, more than one round of 512-row chunks
+    # (768) and at least 48 streams: 256-row chunks (8 rows per lane)
+    assert wb(8, 12, 4096, 64, _lib.KDECAY_F32) == words(8, 12, 4096, 64, 192, 16)  # 1536 chunks at 512 rows
+    assert wb(5, 12, 4096, 64, _lib.KDECAY_F32) == words(5, 12, 4096, 64, 120, 16)  # 960
+    assert wb(4, 12, 4096, 64, _lib.KDECAY_F32) == words(4, 12, 4096, 64, 96, 8)  # 768, one round: 512 rows
+    assert wb(12, 12, 4096, 32, _lib.KDECAY_F32) == words(12, 12, 4096, 32, 144, 8)  # one group: 512 rows
+    assert wb(2, 16, 32768, 128, _lib.KDECAY_BF16) == words(2, 16, 32768, 128, 64, 128)  # 64 streams of 128 B
+    assert wb(1, 16, 65536, 128, _lib.KDECAY_F32) == words(1, 16, 65536, 128, 64, 256)  # four groups of 32 fp32
+
 
 def test_saved_states_floats(kdecay_lib):
     """The training forward's buffer for the backward: the state at each backward
@@ -147,6 +159,7 @@ def test_saved_states_floats(kdecay_lib):
     assert sf(2, 6, 100, 64, _lib.KDECAY_BF16) == 0  # one chunk per stream
     assert sf(2, 6, 4096, 48, _lib.KDECAY_BF16) == 0  # unsupported D
     assert sf(8, 12, 4096, 64, _lib.KDECAY_F64) == 0  # no float64 training kernels
+    assert sf(8, 12, 4096, 64, _lib.KDECAY_F32) == 8 * 12 * 64 * (4096 // 256) + 2 * 12 * 4096  # 256-row chunks
 
 
 def _scan(lib, v_dtype=_lib.KDECAY_BF16, out_dtype=None, D=64, N=4096, vstr=None, ostr=None,

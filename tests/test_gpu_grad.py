@@ -570,3 +570,26 @@ def test_backward_float64_runs_the_fp32_kernels(hip_device, kdecay_lib):
     rdv, rdl, _ = oracle_grads(lam, V, gy)
     assert rel_err(Vd.grad.cpu(), rdv) <= 1e-5
     assert rel(ld.grad.cpu(), rdl) <= 1e-4
+
+
+@pytest.mark.parametrize("B,H,N,D,dname", [(5, 12, 4096, 64, "f32"), (1, 16, 16384, 128, "f32"),
+                                           (1, 12, 16384, 256, "bf16")])
+def test_backward_256_row_chunks_of_multi_group_heads(hip_device, kdecay_lib, B, H, N, D, dname):
+    """Heads of two or more 128-byte channel groups on more than one round of
+    512-row chunks with at least 48 streams take 256-row chunks (8 rows per
+    lane) in several rounds: fp32 D=64 (1920 chunks), fp32 D=128 with chains
+    of 64, bf16 D=256 on 128-byte groups (chains of 64); against the
+    oracle's float64 adjoint recurrence, with carry-in, final-state gradient
+    and offset."""
+    dtype = DTYPES[dname]
+    g = torch.Generator().manual_seed(700 + D + B)
+    lam = lam_uniform(H, 0.5, 0.999, g)
+    V = torch.randn(B, H, N, D, generator=g).to(dtype)
+    gy = torch.randn(B, H, N, D, generator=g).to(dtype)
+    init = torch.randn(B, H, D, generator=g)
+    gfin = torch.randn(B, H, D, generator=g)
+    assert _lib.load().kdecay_scan_bwd_workspace_bytes(B, H, N, D, {torch.float32: _lib.KDECAY_F32,
+                                                                      torch.bfloat16: _lib.KDECAY_BF16}[dtype]) > 0
+    dv, dl, di = gpu_grads(lam, V, gy, hip_device, init=init, gfin=gfin, t_offset=37)
+    rdv, rdl, rdi = O.scan_grads_f64(lam, V, gy, init_state=init, gfin=gfin, t_offset=37)
+    check(dv, dl, di, rdv, rdl, rdi, dtype, f"{dname} B={B} H={H} N={N} D={D}")
