@@ -15,7 +15,8 @@ from tests.decay_cases import lam_uniform
 
 pytestmark = pytest.mark.gpu
 
-CODE = {torch.float32: _lib.KDECAY_F32, torch.bfloat16: _lib.KDECAY_BF16, torch.float16: _lib.KDECAY_F16}
+CODE = {torch.float32: _lib.KDECAY_F32, torch.bfloat16: _lib.KDECAY_BF16, torch.float16: _lib.KDECAY_F16,
+        torch.float64: _lib.KDECAY_F64}
 
 
 def _both(lib, lam, V, init, t_offset, stream):
@@ -49,7 +50,8 @@ def test_noalloc_matches_workspace_entry_point(hip_device, kdecay_lib):
     # each call smaller than the previous one: the array keeps the larger
     # call's words and its epoch, which the next call must not take for its own
     cases = [(8, 12, 4096, 64, torch.bfloat16, False), (2, 3, 1500, 64, torch.bfloat16, True),
-             (1, 4, 3000, 128, torch.float32, False), (1, 2, 700, 32, torch.float16, True),
+             (1, 4, 3000, 128, torch.float32, False), (1, 6, 2048, 64, torch.float64, True),
+             (1, 2, 700, 32, torch.float16, True),
              (1, 1, 100, 64, torch.bfloat16, False)]
     for k, (B, H, N, D, dt, carry) in enumerate(cases):
         print(f"  noalloc call {k}: B={B} H={H} N={N} D={D} {dt} carry={carry}", flush=True)
