@@ -313,6 +313,16 @@ __device__ __forceinline__ u64 peek(const u64* p) {
 // exits normally and flags the header instead of hanging.
 constexpr int kSpinLimit = 1 << 20;
 
+// Look-back window.  When every workgroup of a launch is resident at once, a
+// wider window resolves the chunk chains in fewer polls; when the launch runs
+// in several rounds, the chunks a workgroup waits on have mostly finished in
+// an earlier round, and reading fewer words per poll wins.  Measured (bf16,
+// same-box A/B): B=8 N=4096 H=12 D=64 (768 chunks, one round) window 4
+// 18.3 us, 2 18.5 us; B=1 N=65536 H=16 D=128 (4096 chunks, four rounds)
+// window 4 96.0 us, 3 94.5 us, 2 93.4 us.
+constexpr int kW = 4;        // the whole grid resident at once
+constexpr int kWRounds = 2;  // several rounds
+
 // Look-back words of the W chunks before chunk c (c >= 1) for channel d:
 // w[k] = word of chunk c-1-k.  The reads are unconditional (a load under a
 // branch is waited for at the branch join): where c-1-k < 0 the word of chunk
@@ -1205,7 +1215,15 @@ struct ChunkBwd {
     // rows, at most two rows' stores in flight per wavefront, as in the
     // forward (re-measured on shared buffers, us, none / 1 / 2 / 4 rows in
     // flight: C2 28.51 / 27.03 / 27.06 / 27.93, B=24 N=1024 H=16 28.80 /
-    // 27.19 / 27.37 / 28.04, C4 145.5 / 146.4 / 145.8 / 145.7).
+    // 27.19 / 27.37 / 28.04, C4 145.5 / 146.4 / 145.8 / 145.7), but only
+    // when the grid is resident at once: in several rounds a workgroup's slot
+    // goes to the next round's only once its stores are done, and those
+    // wait behind the next round's reads (stamps at B=16 N=4096 H=12 D=64,
+    // two rounds: 7 us from the first-round dV pass to the workgroup's end,
+    // against 1.5-3 us in one round).  Unthrottled there (same-box A/B on
+    // shared buffers, us, bf16, N=4096 H=12 unless given): D=64 B=16 59.68
+    // -> 57.72, B=24 87.95 -> 86.99, B=32 110.05 -> 108.42; D=128 B=8 59.29
+    // -> 58.46; C4 145.89 -> 145.50; identical outputs.
     if constexpr (LPR >= 8) {
       if (li == R - 1 && (fin_i < 0 || fin_i == R - 1)) {
 #pragma unroll
@@ -1221,7 +1239,7 @@ struct ChunkBwd {
             for (int j = 0; j < VW; ++j) gn[j] += sm.gfin[ds * VW + j];
           }
           store_vec<T, VW>(dp + (int64_t)i * a.dn, gn);
-          if constexpr (R >= 16) {
+          if constexpr (R >= 16 && W != kWRounds) {
             if (i <= R - 3) wait_vmcnt<2>();
           }
           pin(gn);
@@ -1778,16 +1796,6 @@ bool fwd_dtype_ok(int dt) { return dtype_ok(dt) || dt == KDECAY_F64; }
 constexpr int kR = 16;
 constexpr int kNW = 4;
 constexpr int kWPE = 2;
-
-// Look-back window.  When every workgroup of a launch is resident at once, a
-// wider window resolves the chunk chains in fewer polls; when the launch runs
-// in several rounds, the chunks a workgroup waits on have mostly finished in
-// an earlier round, and reading fewer words per poll wins.  Measured (bf16,
-// same-box A/B): B=8 N=4096 H=12 D=64 (768 chunks, one round) window 4
-// 18.3 us, 2 18.5 us; B=1 N=65536 H=16 D=128 (4096 chunks, four rounds)
-// window 4 96.0 us, 3 94.5 us, 2 93.4 us.
-constexpr int kW = 4;        // the whole grid resident at once
-constexpr int kWRounds = 2;  // several rounds
 
 // Compute units of the current device, cached per device (0 if unknown).
 int cu_count() {
