@@ -214,13 +214,22 @@ def test_chunk_size_switch_short_chains(hip_device, kdecay_lib, B, N, nchunk):
     ("bf16", 6, 12, 4096, 128, True),   # 1152
     ("f32", 8, 12, 4096, 64, True),     # 1536 in two groups of 32 fp32 channels
     ("f16", 16, 12, 4096, 64, True),
+    # heads of four or more groups: 256-row chunks from 1024 chunks of 512 rows up, 32 or fewer per stream
+    ("bf16", 2, 12, 4096, 256, False),  # 768: below a full round
+    ("bf16", 4, 8, 4096, 256, True),    # 1024
+    ("bf16", 2, 4, 16384, 256, True),   # 1024 in chains of 32
+    ("bf16", 2, 4, 16896, 256, False),  # 1056 in chains of 33
+    ("bf16", 8, 12, 4096, 192, False),  # three groups per head (2304)
+    ("f32", 8, 12, 4096, 128, True),    # four groups of 32 fp32 channels (3072, four rounds)
 ])
 def test_chunk_shape_just_above_one_round(hip_device, kdecay_lib, dname, B, H, N, D, six):
     """The switch to 256-row chunks at six workgroups per compute unit for
     16-row grids just above one resident round (more than 1280 chunks, or 1024
     with several channel groups per head, up to 1536, 8 or fewer per stream),
-    both sides of each bound, against the oracle; with a carried state, an
-    offset and the final state, and for bf16 also the fp32 output."""
+    and for heads of four or more channel groups at 1024 chunks or more with
+    32 or fewer per stream, both sides of each bound, against the oracle; with
+    a carried state, an offset and the final state, and for bf16 also the
+    fp32 output."""
     dt = DTYPES[dname]
     es = torch.empty((), dtype=dt).element_size()
     rows = chunk_rows(dt, D, 8 if six else 16)
