@@ -218,7 +218,11 @@ size_t kdecay_scan_saved_states_floats(int64_t B, int64_t H, int64_t N,
  *                64 bf16/fp16, D >= 32 fp32), 1024 for 64 bytes, 2048 for 32
  *                bytes; a quarter of that for small grids; 256 rows of whole
  *                256-byte rows for bf16/fp16 heads with a multiple of 128
- *                channels on large grids with chains of at most 32 chunks.
+ *                channels on large grids with chains of at most 32 chunks;
+ *                256 rows of a 128-byte group for heads of two or more such
+ *                groups on grids of more than one round with at least 48
+ *                streams.  (These sizes are reported, not needed: the
+ *                library applies the limit itself.)
  *   lam, init_state, t_offset   as given to the forward call (the row terms
  *                come from the states buffer, computed with the forward's
  *                lam and t_offset)
