@@ -221,8 +221,8 @@ size_t kdecay_scan_saved_states_floats(int64_t B, int64_t H, int64_t N,
  *                channels on large grids with chains of at most 32 chunks;
  *                256 rows of a 128-byte group for heads of two or more such
  *                groups on grids of more than one round with at least 48
- *                streams.  (These sizes are reported, not needed: the
- *                library applies the limit itself.)
+ *                streams.  (The library checks the limit itself; these
+ *                sizes say which row strides it accepts.)
  *   lam, init_state, t_offset   as given to the forward call (the row terms
  *                come from the states buffer, computed with the forward's
  *                lam and t_offset)
