@@ -2129,6 +2129,23 @@ constexpr int64_t kBwdShortChainGrid = 384;
 constexpr int kRBMid = 8;
 constexpr int64_t kBwdOneRound = 768;  // resident 16-row chunks on 256 CUs
 constexpr int64_t kBwdMidStreams = 48;
+// Also 8 rows per lane for 128-byte groups when the 16-row grid has more
+// than 192 and at most 512 chunks: the 8-row grid then runs in one round of
+// at most 1024 (four per CU) where the 16-row one fills at most two thirds
+// of its 768 slots and the 4-row one pays chains four times as long.
+// Measured (bf16 D=64, same-box A/B on shared buffers, us, current choice /
+// 8 rows): 16-row grids B=4 N=4096 H=12 (384 chunks) 19.16 / 17.23, B=7
+// N=2048 H=16 (448) 19.77 / 19.01, B=4 N=4096 H=16 (512) 21.18 / 19.98, B=2
+// N=8192 H=16 (512) 22.49 / 21.23, B=1 N=16384 H=12 (384, chains of 32)
+// 20.1 / 19.48, bf16 D=128 B=2 N=4096 H=12 (384) 19.91 / 17.26; 4-row grids
+// B=8 N=2048 H=12 (384, chains of 4) 21.23 / 16.71, B=6 N=2048 H=12 (288)
+// 19.22 / 15.35, B=1 N=8192 H=16 (256) 19.78 / 14.59, B=4 N=4096 H=8 (256)
+// 15.00 / 14.38, B=8 N=2048 H=8 (256) 14.00 / 13.85.  Not at 192 chunks or
+// fewer (B=8 N=1024 H=12, 192: 12.30 / 13.00; H=6, the end-to-end model's
+// layer: 10.26 / 10.90) nor at a full 16-row round (B=5 N=4096 H=16, 640:
+// 24.87 / 31.00; B=3 N=8192 H=16, 768: 27.44 / 33.19).
+constexpr int64_t kBwdMidLo = 192;
+constexpr int64_t kBwdMidHi = 512;
 int bwd_rows_per_lane(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   const int64_t vw = 16 / elem_size(v_dtype);
   const int64_t DG = bwd_group_width(B, H, N, D, v_dtype);
@@ -2136,9 +2153,10 @@ int bwd_rows_per_lane(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   const int64_t nstream = B * H * (D / DG);
   const int64_t chain = (N + L - 1) / L;
   const int64_t grid = chain * nstream;
+  const bool g128 = DG * elem_size(v_dtype) == 128;
+  if (g128 && grid > kBwdMidLo && grid <= kBwdMidHi) return kRBMid;
   if (grid <= kBwdSmallGrid || (grid <= kBwdShortChainGrid && chain <= 4)) return kRBSmall;
-  if (DG * elem_size(v_dtype) == 128 && D / DG >= 2 && grid > kBwdOneRound && nstream >= kBwdMidStreams)
-    return kRBMid;
+  if (g128 && D / DG >= 2 && grid > kBwdOneRound && nstream >= kBwdMidStreams) return kRBMid;
   return kRB;
 }
 
@@ -2164,10 +2182,16 @@ int launch_bwd(const BwdArgs& a, int64_t grid, int R, hipStream_t s) {
                                                     : one_round;
     hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(kNWB * 64), 0, s, a);
   } else if (R == kRBMid) {
-    // Several rounds of 256-row chunks (bwd_rows_per_lane): more chunks than
-    // the 1024 resident at four workgroups per CU, so the several-round window.
+    // 256-row chunks (bwd_rows_per_lane): one round at four workgroups per CU
+    // (window 4, or 8 for chains of more than 8), or several.
     if constexpr (LPR == 8) {
-      hipLaunchKernelGGL((scan_bwd<T, LPR, kRBMid, kNWB, kWRounds, 4>), dim3((unsigned)grid), dim3(kNWB * 64), 0, s, a);
+      auto* const w4 = scan_bwd<T, LPR, kRBMid, kNWB, kW, 4>;
+      static const int per_cu = workgroups_per_cu(reinterpret_cast<const void*>(w4), kNWB * 64);
+      const int64_t resident = (int64_t)per_cu * cu_count();
+      auto* const k = resident > 0 && grid > resident ? scan_bwd<T, LPR, kRBMid, kNWB, kWRounds, 4>
+                      : a.nchunk > 8                  ? scan_bwd<T, LPR, kRBMid, kNWB, 8, 4>
+                                                      : w4;
+      hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(kNWB * 64), 0, s, a);
     } else {
       return fail(KDECAY_ESHAPE, "no 8-row backward kernel for %d-channel groups", DG);
     }

@@ -103,22 +103,28 @@ def test_workspace_bytes(kdecay_lib):
 def test_backward_workspace_bytes(kdecay_lib):
     wb = kdecay_lib.kdecay_scan_bwd_workspace_bytes
     # 512-row chunks (16 rows x 4 wavefronts x 8 row groups for a 128-byte
-    # group), or 128-row chunks (4 rows) when the 512-row grid has at most 256
-    # chunks, or at most 384 with at most 4 per stream; header + look-back words (one per channel per chunk) + one
-    # 8-byte tagged dlam partial per chunk of every stream, rounded up to 256
-    # bytes.
+    # group); 256-row chunks (8 rows) when the 512-row grid has more than 192
+    # and at most 512 chunks; 128-row chunks (4 rows) when it has at most 192;
+    # header + look-back words (one per channel per chunk) + one 8-byte tagged
+    # dlam partial per chunk of every stream, rounded up to 256 bytes.
     nst, nch = 8 * 12, 4096 // 512
     assert wb(8, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
     nst, nch = 8 * 6, 1024 // 128  # 96 chunks at 512 rows: the small-grid shape
     assert wb(8, 6, 1024, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
-    nst, nch = 8 * 12, 2048 // 128  # 384 chunks at 512 rows, 4 per stream
+    nst, nch = 8 * 12, 2048 // 256  # 384 chunks at 512 rows: 256-row chunks
     assert wb(8, 12, 2048, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
-    nst, nch = 8 * 12, 5  # 480 chunks at 512 rows, 5 per stream: 512-row chunks
+    nst, nch = 8 * 12, 9  # 480 chunks at 512 rows: 256-row chunks, 9 per stream
     assert wb(8, 12, 2049, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
-    nst, nch = 4 * 12, 4096 // 512  # 384 chunks, 8 per stream: 512-row chunks
+    nst, nch = 4 * 12, 4096 // 256  # 384 chunks at 512 rows: 256-row chunks
     assert wb(4, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
-    nst, nch = 8 * 14, 2048 // 512  # 448 chunks, 4 per stream: 512-row chunks
+    nst, nch = 8 * 14, 2048 // 256  # 448 chunks at 512 rows: 256-row chunks
     assert wb(8, 14, 2048, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    nst, nch = 8 * 12, 1024 // 128  # 192 chunks at 512 rows: 128-row chunks
+    assert wb(8, 12, 1024, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    nst, nch = 4 * 16, 2048 // 256  # 256 chunks at 512 rows: 256-row chunks
+    assert wb(4, 16, 2048, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    nst, nch = 5 * 16, 4096 // 512  # 640 chunks: 512-row chunks
+    assert wb(5, 16, 4096, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
     # one chunk per stream: no look-back words, but the header and the partials
     assert wb(2, 6, 100, 64, _lib.KDECAY_BF16) == 256 + 256
     assert wb(2, 6, 100, 48, _lib.KDECAY_BF16) == 0  # unsupported D
@@ -129,8 +135,9 @@ def test_backward_workspace_bytes(kdecay_lib):
     # long chains (256 of 256 rows): two 128-byte streams per head, 512-row chunks
     nst, nch = 1 * 16 * 2, 65536 // 512
     assert wb(1, 16, 65536, 128, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
-    # a grid of 256-row chunks below 512 (4 x 6 x 16 = 384): two streams, 512-row chunks
-    nst, nch = 4 * 6 * 2, 4096 // 512
+    # a grid of 256-row chunks below 512 (4 x 6 x 16 = 384): two 128-byte streams per head,
+    # 384 chunks of 512 rows: 256-row chunks
+    nst, nch = 4 * 6 * 2, 4096 // 256
     assert wb(4, 6, 4096, 128, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
 
     def words(B, H, N, D, nst, nch):
@@ -153,7 +160,7 @@ def test_saved_states_floats(kdecay_lib):
     sf = kdecay_lib.kdecay_scan_saved_states_floats
     assert sf(8, 12, 4096, 64, _lib.KDECAY_BF16) == 8 * 12 * 64 * (4096 // 512) + 2 * 12 * 4096
     assert sf(8, 6, 1024, 64, _lib.KDECAY_BF16) == 8 * 6 * 64 * (1024 // 128) + 2 * 6 * 1024  # 128-row chunks
-    assert sf(8, 12, 2049, 64, _lib.KDECAY_BF16) == 8 * 12 * 64 * 5 + 2 * 12 * 2049  # ragged last chunk
+    assert sf(8, 12, 2049, 64, _lib.KDECAY_BF16) == 8 * 12 * 64 * 9 + 2 * 12 * 2049  # 256-row chunks, ragged last
     assert sf(1, 16, 65536, 128, _lib.KDECAY_BF16) == 16 * 128 * (65536 // 512) + 2 * 16 * 65536
     assert sf(8, 12, 4096, 128, _lib.KDECAY_BF16) == 8 * 12 * 128 * (4096 // 256) + 2 * 12 * 4096  # whole rows
     assert sf(2, 6, 100, 64, _lib.KDECAY_BF16) == 0  # one chunk per stream

@@ -317,8 +317,12 @@ def test_backward_dlam_one_head_many_terms(hip_device, kdecay_lib):
     """dlam of a single head summed over 45 x 1388 x 128 = 8 M terms of both
     signs (bf16, a random parity sweep's case): its value, -2.636, is a small
     remainder of the terms, so the sums' precision decides its digits.  The
-    reference's fp32 path is 1.3e-4 off the fp64 adjoint here; the chunk
-    partials summed in fp32 were 1.9e-4 off, summed in double 1.9e-6."""
+    reference's fp32 path is 1.3e-4 off the fp64 adjoint here.  This grid
+    (270 chunks of 512 rows) takes 256-row chunks (8 rows per lane): 9.4e-5
+    off, with the chunk partials, wavefront and workgroup sums in double (in
+    fp32 they were 1.9e-4 off).  What remains is the lanes' fp32 states and
+    row sums over their rows: 4 rows per lane measured 1.9e-6, 16 rows
+    2.2e-4.  Bound: no worse than the reference's fp32 path."""
     B, H, N, D = 45, 1, 1388, 128
     g = torch.Generator().manual_seed(937 + 50000)
     lam = (0.3 + (0.9999 - 0.3) * torch.rand(H, generator=g)).float()
@@ -327,7 +331,7 @@ def test_backward_dlam_one_head_many_terms(hip_device, kdecay_lib):
     print(f"  dlam over one head: bf16 {B}x{H}x{N}x{D}", flush=True)
     dv, dl, _ = gpu_grads(lam, V, gy, hip_device)
     rdv, rdl, _ = O.scan_grads_f64(lam, V, gy)
-    assert rel(dl, rdl) <= 2e-5, f"dlam rel {rel(dl, rdl):.3e}"
+    assert rel(dl, rdl) <= 1.3e-4, f"dlam rel {rel(dl, rdl):.3e}"
     check(dv, dl, None, rdv, rdl, None, torch.bfloat16, "one head")
 
 
@@ -592,4 +596,30 @@ def test_backward_256_row_chunks_of_multi_group_heads(hip_device, kdecay_lib, B,
                                                                       torch.bfloat16: _lib.KDECAY_BF16}[dtype]) > 0
     dv, dl, di = gpu_grads(lam, V, gy, hip_device, init=init, gfin=gfin, t_offset=37)
     rdv, rdl, rdi = O.scan_grads_f64(lam, V, gy, init_state=init, gfin=gfin, t_offset=37)
+    check(dv, dl, di, rdv, rdl, rdi, dtype, f"{dname} B={B} H={H} N={N} D={D}")
+
+
+@pytest.mark.parametrize("B,H,N,D,dname", [(8, 12, 2048, 64, "bf16"), (1, 16, 8192, 64, "bf16"),
+                                           (4, 12, 2048, 64, "f32")])
+def test_backward_one_round_of_256_row_chunks(hip_device, kdecay_lib, B, H, N, D, dname):
+    """Grids of more than 192 and at most 512 chunks of 512 rows (128-byte
+    groups) take 256-row chunks in one round: bf16 at 384 chunks, at 256 in
+    chains of 32 (the window-8 kernel), and fp32 with two groups per head;
+    against the oracle's float64 adjoint recurrence, with carry-in,
+    final-state gradient and offset."""
+    dtype = DTYPES[dname]
+    code = {torch.float32: _lib.KDECAY_F32, torch.bfloat16: _lib.KDECAY_BF16}[dtype]
+    nst = B * H * (D * torch.empty((), dtype=dtype).element_size() // 128)
+    # the workspace holds one look-back word per channel per 256-row chunk
+    nch = -(-N // 256)
+    assert _lib.load().kdecay_scan_bwd_workspace_bytes(B, H, N, D, code) == \
+        256 + B * H * nch * D * 8 + (nst * nch * 8 + 255) // 256 * 256
+    g = torch.Generator().manual_seed(720 + B + N)
+    lam = lam_uniform(H, 0.5, 0.999, g)
+    V = torch.randn(B, H, N, D, generator=g).to(dtype)
+    gy = torch.randn(B, H, N, D, generator=g).to(dtype)
+    init = torch.randn(B, H, D, generator=g)
+    gfin = torch.randn(B, H, D, generator=g)
+    dv, dl, di = gpu_grads(lam, V, gy, hip_device, init=init, gfin=gfin, t_offset=11)
+    rdv, rdl, rdi = O.scan_grads_f64(lam, V, gy, init_state=init, gfin=gfin, t_offset=11)
     check(dv, dl, di, rdv, rdl, rdi, dtype, f"{dname} B={B} H={H} N={N} D={D}")
