@@ -282,10 +282,14 @@ typedef unsigned long long u64;
 //          give-up, words of the launch that gave up may carry a later
 //          launch's tag, so only a cleared workspace computes again.
 //   DONE   workgroups of the running launch that have counted toward the
-//          epoch's advance (the forward: each stream's last chunk; the
-//          backward: see ChunkBwd::run)
+//          epoch's advance (the forward: each stream's last chunk, directly
+//          or through a sub-count; the backward: see ChunkBwd::run)
+// From byte 256: kCountSlots sub-counts, 32 bytes apart (count_done_2).
 enum { HDR_EPOCH = 0, HDR_ERROR = 1, HDR_DONE = 2 };
-constexpr size_t kHeaderBytes = 256;
+constexpr unsigned kCountSlots = 64;
+constexpr unsigned kCountBase = 64;    // word index of the first sub-count (byte 256)
+constexpr unsigned kCountStride = 8;   // words between sub-counts (32 bytes)
+constexpr size_t kHeaderBytes = 4 * (kCountBase + kCountSlots * kCountStride);  // 2304
 
 // The epoch and the error word of a workspace header, as one load.
 struct EpochErr {
@@ -552,6 +556,34 @@ __device__ __forceinline__ void count_done(unsigned* hdr, unsigned n, unsigned e
   }
 }
 
+// count_done for n workgroups numbered s = 0..n-1 in two levels: workgroup s
+// counts on sub-count s % kCountSlots, and the one that completes a sub-count
+// counts on DONE (min(n, kCountSlots) of them).  With every count on one word
+// the n atomics of a launch queue on that word at the launch's end.  Measured
+// (the forward, bf16 D=64, same-box A/B, us, one word / 64 sub-counts 32
+// bytes apart): B=128 N=512 H=12 (1536 streams) 106.6 / 42.7, B=64 N=4096
+// H=12 (768) 171.3 / 143.5, B=64 N=1024 H=12 44.1 / 39.4, B=40 N=4096 H=16
+// (640) 132.5 / 120.6, B=48 N=4096 H=12 (576) 117.2 / 110.8; 16 sub-counts in
+// one 64-byte segment did not help (109.6 at 1536 streams), 16 of them 256
+// bytes apart nearly did (46.3).  With fewer streams the second atomic is the
+// cost: B=16 N=4096 H=12 (192 streams) 38.4 / 38.7, B=8 (96) 17.36 / 17.59;
+// between them no gain (B=20, 24, 32 H=12: 48.6 / 48.7, 57.8 / 57.7, 72.2 /
+// 72.0; B=16 H=16, 256 streams: 46.6 / 47.1).
+__device__ __forceinline__ void count_done_2(unsigned* hdr, unsigned n, unsigned s, unsigned epoch) {
+  const unsigned k = s % kCountSlots;
+  const unsigned nk = n / kCountSlots + (k < n % kCountSlots ? 1u : 0u);
+  unsigned* c = hdr + kCountBase + k * kCountStride;
+  const unsigned d = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (d == nk - 1u) {
+    __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    count_done(hdr, n < kCountSlots ? n : kCountSlots, epoch);
+  }
+}
+
+// Streams up to which the forward counts each stream's last chunk on DONE
+// directly (count_done_2 above it).
+constexpr int kFwdPerStreamCount = 384;
+
 __device__ __forceinline__ EpochErr read_epoch_v(const unsigned* hdr) {
   unsigned zero;
   asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
@@ -812,7 +844,12 @@ struct ChunkScan {
     // workgroup of this launch has read the epoch (each holds at least one
     // item): advance it for the next launch.  (Counted after the stores
     // instead, C2 measured 1.7% slower and the small grids 2.5%.)
-    if (multi && last && tid == 0 && !poisoned) count_done(a.hdr, (unsigned)a.nstream, eh.epoch);
+    if (multi && last && tid == 0 && !poisoned) {
+      if (a.nstream <= kFwdPerStreamCount)
+        count_done(a.hdr, (unsigned)a.nstream, eh.epoch);
+      else
+        count_done_2(a.hdr, (unsigned)a.nstream, (unsigned)stream, eh.epoch);
+    }
 
     // The lane's true start state.
     float ew[VW];  // state before this wavefront's first row, zero carry into the chunk

@@ -10,6 +10,10 @@ from __future__ import annotations
 
 import torch
 
+# Bytes of a scan workspace's header: launch epoch, completion count and sticky
+# error word, then 64 completion sub-counts 32 bytes apart from byte 256.
+WORKSPACE_HEADER_BYTES = 2304
+
 
 def lam_from_uniform(u: torch.Tensor) -> torch.Tensor:
     """lam = sigmoid(log_lambda) with log_lambda = logit(u), as the layer computes it."""

@@ -12,6 +12,7 @@ import pytest
 import torch
 
 from kilat_amd import _build, _lib
+from tests.decay_cases import WORKSPACE_HEADER_BYTES as HDR
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "kdecay.h")
@@ -54,50 +55,50 @@ def test_workspace_bytes(kdecay_lib):
     # input: 512 rows of a 128-byte group, or half that (8 rows per lane instead of
     # 16) when the 16-row grid has at most 416 chunks (640 with 2 chunks per stream,
     # 160 with 1).  Words: one per channel per chunk.
-    assert ws(8, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + 8 * 12 * 8 * 64 * 8  # 768 chunks
-    assert ws(1, 16, 65536, 128, _lib.KDECAY_BF16) == 256 + 16 * 128 * 128 * 8  # 4096 chunks
-    assert ws(2, 6, 512, 64, _lib.KDECAY_BF16) == 256 + 2 * 6 * 2 * 64 * 8  # small grid: 256-row chunks
+    assert ws(8, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 8 * 12 * 8 * 64 * 8  # 768 chunks
+    assert ws(1, 16, 65536, 128, _lib.KDECAY_BF16) == HDR + 16 * 128 * 128 * 8  # 4096 chunks
+    assert ws(2, 6, 512, 64, _lib.KDECAY_BF16) == HDR + 2 * 6 * 2 * 64 * 8  # small grid: 256-row chunks
     assert ws(2, 6, 256, 64, _lib.KDECAY_BF16) == 0  # one chunk per stream
     # float64: 16-channel groups, 8 lanes per row as fp32's 32-channel groups, so
     # D fp64 channels make the streams and chunks of 2D fp32 channels, with half
     # the channels' words
     for B, H, N, D in ((8, 12, 4096, 64), (2, 6, 512, 16), (1, 16, 65536, 128), (2, 3, 3000, 48)):
-        assert ws(B, H, N, D, _lib.KDECAY_F64) - 256 == (ws(B, H, N, 2 * D, _lib.KDECAY_F32) - 256) // 2 > 0
+        assert ws(B, H, N, D, _lib.KDECAY_F64) - HDR == (ws(B, H, N, 2 * D, _lib.KDECAY_F32) - HDR) // 2 > 0
     assert ws(2, 6, 128, 16, _lib.KDECAY_F64) == 0  # one chunk per stream
     # heads of four or more 128-byte groups, a full round of 512-row chunks or more and at
     # most 32 per stream: 256-row chunks (the six-per-CU kernel)
-    assert ws(8, 12, 4096, 256, _lib.KDECAY_BF16) == 256 + 8 * 12 * 16 * 256 * 8  # 3072 chunks at 512 rows
-    assert ws(2, 16, 16384, 256, _lib.KDECAY_BF16) == 256 + 2 * 16 * 64 * 256 * 8  # 32 per stream
-    assert ws(1, 16, 32768, 256, _lib.KDECAY_BF16) == 256 + 16 * 64 * 256 * 8  # 64 per stream: 512 rows
-    assert ws(2, 12, 4096, 256, _lib.KDECAY_BF16) == 256 + 2 * 12 * 8 * 256 * 8  # 768 chunks: 512 rows
-    assert ws(8, 12, 4096, 192, _lib.KDECAY_BF16) == 256 + 8 * 12 * 8 * 192 * 8  # three groups: 512 rows
-    assert ws(2, 6, 1024, 64, _lib.KDECAY_F32) == 256 + 2 * 6 * 4 * 64 * 8  # 2 groups of 32, 256-row chunks
-    assert ws(1, 2, 4096, 32, _lib.KDECAY_BF16) == 256 + 2 * 8 * 32 * 8  # 32-channel rows: 512-row chunks
-    assert ws(8, 12, 2048, 64, _lib.KDECAY_BF16) == 256 + 8 * 12 * 8 * 64 * 8  # 384 chunks at 16 rows: 8
-    assert ws(4, 13, 4096, 64, _lib.KDECAY_BF16) == 256 + 4 * 13 * 16 * 64 * 8  # 416 chunks at 16 rows: 8
-    assert ws(4, 13, 4097, 64, _lib.KDECAY_BF16) == 256 + 4 * 13 * 9 * 64 * 8  # 468: 16 rows
-    assert ws(20, 16, 1024, 64, _lib.KDECAY_BF16) == 256 + 20 * 16 * 4 * 64 * 8  # 640, 2 per stream: 8 rows
-    assert ws(21, 16, 1024, 64, _lib.KDECAY_BF16) == 256 + 21 * 16 * 2 * 64 * 8  # 672: 16 rows
-    assert ws(10, 16, 512, 64, _lib.KDECAY_BF16) == 256 + 10 * 16 * 2 * 64 * 8  # 160, 1 per stream: 8 rows
+    assert ws(8, 12, 4096, 256, _lib.KDECAY_BF16) == HDR + 8 * 12 * 16 * 256 * 8  # 3072 chunks at 512 rows
+    assert ws(2, 16, 16384, 256, _lib.KDECAY_BF16) == HDR + 2 * 16 * 64 * 256 * 8  # 32 per stream
+    assert ws(1, 16, 32768, 256, _lib.KDECAY_BF16) == HDR + 16 * 64 * 256 * 8  # 64 per stream: 512 rows
+    assert ws(2, 12, 4096, 256, _lib.KDECAY_BF16) == HDR + 2 * 12 * 8 * 256 * 8  # 768 chunks: 512 rows
+    assert ws(8, 12, 4096, 192, _lib.KDECAY_BF16) == HDR + 8 * 12 * 8 * 192 * 8  # three groups: 512 rows
+    assert ws(2, 6, 1024, 64, _lib.KDECAY_F32) == HDR + 2 * 6 * 4 * 64 * 8  # 2 groups of 32, 256-row chunks
+    assert ws(1, 2, 4096, 32, _lib.KDECAY_BF16) == HDR + 2 * 8 * 32 * 8  # 32-channel rows: 512-row chunks
+    assert ws(8, 12, 2048, 64, _lib.KDECAY_BF16) == HDR + 8 * 12 * 8 * 64 * 8  # 384 chunks at 16 rows: 8
+    assert ws(4, 13, 4096, 64, _lib.KDECAY_BF16) == HDR + 4 * 13 * 16 * 64 * 8  # 416 chunks at 16 rows: 8
+    assert ws(4, 13, 4097, 64, _lib.KDECAY_BF16) == HDR + 4 * 13 * 9 * 64 * 8  # 468: 16 rows
+    assert ws(20, 16, 1024, 64, _lib.KDECAY_BF16) == HDR + 20 * 16 * 4 * 64 * 8  # 640, 2 per stream: 8 rows
+    assert ws(21, 16, 1024, 64, _lib.KDECAY_BF16) == HDR + 21 * 16 * 2 * 64 * 8  # 672: 16 rows
+    assert ws(10, 16, 512, 64, _lib.KDECAY_BF16) == HDR + 10 * 16 * 2 * 64 * 8  # 160, 1 per stream: 8 rows
     assert ws(11, 16, 512, 64, _lib.KDECAY_BF16) == 0  # 176 single-chunk streams: 16 rows, no look-back
     assert ws(2, 6, 1024, 48, _lib.KDECAY_BF16) == 0  # unsupported D
     # Just above one resident round of 512-row chunks (8 or fewer per stream, full
     # 128-byte groups): 256-row chunks, six workgroups per compute unit.
-    assert ws(13, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + 13 * 12 * 8 * 64 * 8  # 1248: 16 rows
-    assert ws(14, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + 14 * 12 * 16 * 64 * 8  # 1344: 8 rows
-    assert ws(16, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + 16 * 12 * 16 * 64 * 8  # 1536: 8 rows
-    assert ws(17, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + 17 * 12 * 8 * 64 * 8  # 1632: 16 rows
-    assert ws(14, 12, 4097, 64, _lib.KDECAY_BF16) == 256 + 14 * 12 * 9 * 64 * 8  # 9 per stream: 16 rows
-    assert ws(5, 12, 4096, 128, _lib.KDECAY_BF16) == 256 + 5 * 12 * 8 * 128 * 8  # 960 in 2 groups: one round, 16 rows
-    assert ws(6, 12, 4096, 128, _lib.KDECAY_BF16) == 256 + 6 * 12 * 16 * 128 * 8  # 1152 in 2 groups: 8 rows
-    assert ws(8, 12, 4096, 64, _lib.KDECAY_F32) == 256 + 8 * 12 * 16 * 64 * 8  # 1536 in 2 groups: 8 rows
+    assert ws(13, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 13 * 12 * 8 * 64 * 8  # 1248: 16 rows
+    assert ws(14, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 14 * 12 * 16 * 64 * 8  # 1344: 8 rows
+    assert ws(16, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 16 * 12 * 16 * 64 * 8  # 1536: 8 rows
+    assert ws(17, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 17 * 12 * 8 * 64 * 8  # 1632: 16 rows
+    assert ws(14, 12, 4097, 64, _lib.KDECAY_BF16) == HDR + 14 * 12 * 9 * 64 * 8  # 9 per stream: 16 rows
+    assert ws(5, 12, 4096, 128, _lib.KDECAY_BF16) == HDR + 5 * 12 * 8 * 128 * 8  # 960 in 2 groups: one round, 16 rows
+    assert ws(6, 12, 4096, 128, _lib.KDECAY_BF16) == HDR + 6 * 12 * 16 * 128 * 8  # 1152 in 2 groups: 8 rows
+    assert ws(8, 12, 4096, 64, _lib.KDECAY_F32) == HDR + 8 * 12 * 16 * 64 * 8  # 1536 in 2 groups: 8 rows
     # Small grids of long streams: from 64 chunks of 256 rows per stream on, 512-row
     # chunks of 8 wavefronts (full 128-byte groups).
-    assert ws(1, 6, 16128, 64, _lib.KDECAY_BF16) == 256 + 6 * 63 * 64 * 8  # 63 per stream: 256 rows
-    assert ws(1, 6, 16384, 64, _lib.KDECAY_BF16) == 256 + 6 * 32 * 64 * 8  # 64: 512 rows
-    assert ws(1, 2, 16384, 64, _lib.KDECAY_F32) == 256 + 2 * 32 * 64 * 8  # two groups of 32 fp32: 512 rows
-    assert ws(1, 2, 65536, 32, _lib.KDECAY_BF16) == 256 + 2 * 128 * 32 * 8  # 64-byte rows keep 4 x 8: 512 rows
-    assert ws(32, 12, 4096, 32, _lib.KDECAY_BF16) == 256 + 32 * 12 * 4 * 32 * 8  # 1536 of 64-byte rows: 1024-row chunks
+    assert ws(1, 6, 16128, 64, _lib.KDECAY_BF16) == HDR + 6 * 63 * 64 * 8  # 63 per stream: 256 rows
+    assert ws(1, 6, 16384, 64, _lib.KDECAY_BF16) == HDR + 6 * 32 * 64 * 8  # 64: 512 rows
+    assert ws(1, 2, 16384, 64, _lib.KDECAY_F32) == HDR + 2 * 32 * 64 * 8  # two groups of 32 fp32: 512 rows
+    assert ws(1, 2, 65536, 32, _lib.KDECAY_BF16) == HDR + 2 * 128 * 32 * 8  # 64-byte rows keep 4 x 8: 512 rows
+    assert ws(32, 12, 4096, 32, _lib.KDECAY_BF16) == HDR + 32 * 12 * 4 * 32 * 8  # 1536 of 64-byte rows: 1024-row chunks
 
 
 def test_backward_workspace_bytes(kdecay_lib):
@@ -108,40 +109,40 @@ def test_backward_workspace_bytes(kdecay_lib):
     # header + look-back words (one per channel per chunk) + one 8-byte tagged
     # dlam partial per chunk of every stream, rounded up to 256 bytes.
     nst, nch = 8 * 12, 4096 // 512
-    assert wb(8, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    assert wb(8, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
     nst, nch = 8 * 6, 1024 // 128  # 96 chunks at 512 rows: the small-grid shape
-    assert wb(8, 6, 1024, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    assert wb(8, 6, 1024, 64, _lib.KDECAY_BF16) == HDR + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
     nst, nch = 8 * 12, 2048 // 256  # 384 chunks at 512 rows: 256-row chunks
-    assert wb(8, 12, 2048, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    assert wb(8, 12, 2048, 64, _lib.KDECAY_BF16) == HDR + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
     nst, nch = 8 * 12, 9  # 480 chunks at 512 rows: 256-row chunks, 9 per stream
-    assert wb(8, 12, 2049, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    assert wb(8, 12, 2049, 64, _lib.KDECAY_BF16) == HDR + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
     nst, nch = 4 * 12, 4096 // 256  # 384 chunks at 512 rows: 256-row chunks
-    assert wb(4, 12, 4096, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    assert wb(4, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
     nst, nch = 8 * 14, 2048 // 256  # 448 chunks at 512 rows: 256-row chunks
-    assert wb(8, 14, 2048, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    assert wb(8, 14, 2048, 64, _lib.KDECAY_BF16) == HDR + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
     nst, nch = 8 * 12, 1024 // 128  # 192 chunks at 512 rows: 128-row chunks
-    assert wb(8, 12, 1024, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    assert wb(8, 12, 1024, 64, _lib.KDECAY_BF16) == HDR + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
     nst, nch = 4 * 16, 2048 // 256  # 256 chunks at 512 rows: 256-row chunks
-    assert wb(4, 16, 2048, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    assert wb(4, 16, 2048, 64, _lib.KDECAY_BF16) == HDR + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
     nst, nch = 5 * 16, 4096 // 512  # 640 chunks: 512-row chunks
-    assert wb(5, 16, 4096, 64, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    assert wb(5, 16, 4096, 64, _lib.KDECAY_BF16) == HDR + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
     # one chunk per stream: no look-back words, but the header and the partials
-    assert wb(2, 6, 100, 64, _lib.KDECAY_BF16) == 256 + 256
+    assert wb(2, 6, 100, 64, _lib.KDECAY_BF16) == HDR + 256
     assert wb(2, 6, 100, 48, _lib.KDECAY_BF16) == 0  # unsupported D
     # 128 bf16 channels on a large grid with short chains: whole 256-byte rows,
     # one stream per head, 256-row chunks (16 per stream, 1536 in all)
     nst, nch = 8 * 12, 4096 // 256
-    assert wb(8, 12, 4096, 128, _lib.KDECAY_BF16) == 256 + nst * nch * 128 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    assert wb(8, 12, 4096, 128, _lib.KDECAY_BF16) == HDR + nst * nch * 128 * 8 + (nst * nch * 8 + 255) // 256 * 256
     # long chains (256 of 256 rows): two 128-byte streams per head, 512-row chunks
     nst, nch = 1 * 16 * 2, 65536 // 512
-    assert wb(1, 16, 65536, 128, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    assert wb(1, 16, 65536, 128, _lib.KDECAY_BF16) == HDR + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
     # a grid of 256-row chunks below 512 (4 x 6 x 16 = 384): two 128-byte streams per head,
     # 384 chunks of 512 rows: 256-row chunks
     nst, nch = 4 * 6 * 2, 4096 // 256
-    assert wb(4, 6, 4096, 128, _lib.KDECAY_BF16) == 256 + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
+    assert wb(4, 6, 4096, 128, _lib.KDECAY_BF16) == HDR + nst * nch * 64 * 8 + (nst * nch * 8 + 255) // 256 * 256
 
     def words(B, H, N, D, nst, nch):
-        return 256 + B * H * nch * D * 8 + (nst * nch * 8 + 255) // 256 * 256
+        return HDR + B * H * nch * D * 8 + (nst * nch * 8 + 255) // 256 * 256
 
     # heads of two or more 128-byte groups, more than one round of 512-row chunks
     # (768) and at least 48 streams: 256-row chunks (8 rows per lane)

@@ -16,6 +16,7 @@ import kilat_amd
 from kilat_amd import _lib
 from oracle import decay_oracle as O
 from tests.decay_cases import lam_uniform, rel_err
+from tests.decay_cases import WORKSPACE_HEADER_BYTES as HDR
 
 pytestmark = pytest.mark.gpu
 
@@ -250,7 +251,7 @@ def test_backward_whole_row_streams(hip_device, kdecay_lib, dname, B, H, N, D):
     code = {"bf16": _lib.KDECAY_BF16, "f16": _lib.KDECAY_F16}[dname]
     nst, nch = B * H * (D // 128), (N + 255) // 256  # one stream per 128 channels, 256-row chunks
     assert kdecay_lib.kdecay_scan_bwd_workspace_bytes(B, H, N, D, code) == \
-        256 + nst * nch * 128 * 8 + (nst * nch * 8 + 255) // 256 * 256
+        HDR + nst * nch * 128 * 8 + (nst * nch * 8 + 255) // 256 * 256
     g = torch.Generator().manual_seed(230 + D + N)
     lam = lam_uniform(H, 0.5, 0.9999, g)
     V = torch.randn(B, H, N, D, generator=g).to(dtype)
@@ -599,6 +600,24 @@ def test_backward_256_row_chunks_of_multi_group_heads(hip_device, kdecay_lib, B,
     check(dv, dl, di, rdv, rdl, rdi, dtype, f"{dname} B={B} H={H} N={N} D={D}")
 
 
+def test_backward_after_training_forward_of_many_streams(hip_device, kdecay_lib):
+    """A training forward of 485 streams (more than 384: its last chunks
+    count through the workspace's sub-counts) saves the states its backward
+    starts from; both against the oracle's float64 adjoint, twice in a row
+    on the same workspaces, with carry-in, final-state gradient and offset."""
+    g = torch.Generator().manual_seed(720)
+    B, H, N, D = 97, 5, 600, 64
+    for rep in range(2):
+        lam = lam_uniform(H, 0.5, 0.999, g)
+        V = torch.randn(B, H, N, D, generator=g).to(torch.bfloat16)
+        gy = torch.randn(B, H, N, D, generator=g).to(torch.bfloat16)
+        init = torch.randn(B, H, D, generator=g)
+        gfin = torch.randn(B, H, D, generator=g)
+        dv, dl, di = gpu_grads(lam, V, gy, hip_device, init=init, gfin=gfin, t_offset=11)
+        rdv, rdl, rdi = O.scan_grads_f64(lam, V, gy, init_state=init, gfin=gfin, t_offset=11)
+        check(dv, dl, di, rdv, rdl, rdi, torch.bfloat16, f"rep {rep} B={B} H={H} N={N} D={D}")
+
+
 @pytest.mark.parametrize("B,H,N,D,dname", [(8, 12, 2048, 64, "bf16"), (1, 16, 8192, 64, "bf16"),
                                            (4, 12, 2048, 64, "f32")])
 def test_backward_one_round_of_256_row_chunks(hip_device, kdecay_lib, B, H, N, D, dname):
@@ -613,7 +632,7 @@ def test_backward_one_round_of_256_row_chunks(hip_device, kdecay_lib, B, H, N, D
     # the workspace holds one look-back word per channel per 256-row chunk
     nch = -(-N // 256)
     assert _lib.load().kdecay_scan_bwd_workspace_bytes(B, H, N, D, code) == \
-        256 + B * H * nch * D * 8 + (nst * nch * 8 + 255) // 256 * 256
+        HDR + B * H * nch * D * 8 + (nst * nch * 8 + 255) // 256 * 256
     g = torch.Generator().manual_seed(720 + B + N)
     lam = lam_uniform(H, 0.5, 0.999, g)
     V = torch.randn(B, H, N, D, generator=g).to(dtype)

@@ -18,6 +18,7 @@ from oracle import c_oracle as C
 from oracle import decay_oracle as O
 from tests.decay_cases import (assert_rounded_once, c1_inputs, c2_inputs, c4_inputs, elementwise_rel, lam_uniform,
                                max_abs, rel_err)
+from tests.decay_cases import WORKSPACE_HEADER_BYTES as HDR
 
 pytestmark = pytest.mark.gpu
 
@@ -170,6 +171,32 @@ def test_mixed_shapes_share_one_workspace(hip_device, kdecay_lib):
     assert kilat_amd.workspace_error(probe) == 0
 
 
+def test_many_streams_count_through_sub_counts(hip_device, kdecay_lib):
+    """Launches of more than 384 streams count their last chunks toward the
+    epoch's advance through 64 sub-counts; fewer streams count on one word.
+    Back-to-back launches on one workspace alternate the two, twice over,
+    with stream counts that are not multiples of 64 (485, 410): each launch
+    must advance the epoch exactly once and leave every sub-count at zero,
+    or a later launch would take older words for its own (or wait for words
+    that never come, and give up).  Each is checked against the oracle,
+    with carry-in and final state."""
+    g = torch.Generator().manual_seed(191)
+    shapes = [(97, 5, 600, 64, torch.bfloat16),   # 485 streams x 2 chunks: sub-counts
+              (4, 12, 2048, 64, torch.bfloat16),  # 48 streams: one word
+              (128, 12, 700, 64, torch.bfloat16),  # 1536 streams x 2 chunks
+              (41, 10, 1500, 32, torch.float32)]  # 410 streams x 3 chunks
+    for k, (B, H, N, D, dt) in enumerate(shapes * 2):
+        lam = lam_uniform(H, 0.5, 0.9999, g)
+        V = torch.randn(B, H, N, D, generator=g).to(dt)
+        init = torch.randn(B, H, D, generator=g)
+        y, fin = gpu_scan(lam, V, hip_device, initial_state=init.to(hip_device), return_final_state=True)
+        ref, sref = C.scan_f32(lam.numpy(), V.float().numpy(), init.numpy(), 0)
+        assert_parity(y.cpu(), torch.from_numpy(ref).to(dt), dt, f"launch {k} {(B, H, N, D, dt)}")
+        assert rel_err(fin.cpu(), torch.from_numpy(sref)) <= 1e-5, f"launch {k} final state"
+    probe = torch.empty(1, 1, 1, 64, device=hip_device)
+    assert kilat_amd.workspace_error(probe) == 0
+
+
 @pytest.mark.parametrize("N", [4096, 4097])
 def test_chunk_size_switch(hip_device, kdecay_lib, N):
     """52 streams of bf16 D=64: N=4096 is exactly 416 chunks of 512 rows (the
@@ -178,7 +205,7 @@ def test_chunk_size_switch(hip_device, kdecay_lib, N):
     lam = lam_uniform(13, 0.5, 0.9999, g)
     V = torch.randn(4, 13, N, 64, generator=g).to(torch.bfloat16)
     ws = kdecay_lib.kdecay_scan_workspace_bytes(4, 13, N, 64, 1)
-    assert ws == 256 + 4 * 13 * (16 if N == 4096 else 9) * 64 * 8
+    assert ws == HDR + 4 * 13 * (16 if N == 4096 else 9) * 64 * 8
     y, fin = gpu_scan(lam, V, hip_device, return_final_state=True)
     ref, sref = O.scan(lam, V)
     assert_parity(y, ref, torch.bfloat16, f"N={N}")
@@ -196,7 +223,7 @@ def test_chunk_size_switch_short_chains(hip_device, kdecay_lib, B, N, nchunk):
     V = torch.randn(B, 16, N, 64, generator=g).to(torch.bfloat16)
     init = torch.randn(B, 16, 64, generator=g)
     ws = kdecay_lib.kdecay_scan_workspace_bytes(B, 16, N, 64, 1)
-    assert ws == (256 + B * 16 * nchunk * 64 * 8 if nchunk else 0)
+    assert ws == (HDR + B * 16 * nchunk * 64 * 8 if nchunk else 0)
     y, fin = gpu_scan(lam, V, hip_device, initial_state=init.to(hip_device), return_final_state=True, t_offset=9)
     ref, sref = O.scan(lam, V, init_state=init, t_offset=9)
     assert_parity(y, ref, torch.bfloat16, f"B={B} N={N}")
@@ -234,7 +261,7 @@ def test_chunk_shape_just_above_one_round(hip_device, kdecay_lib, dname, B, H, N
     es = torch.empty((), dtype=dt).element_size()
     rows = chunk_rows(dt, D, 8 if six else 16)
     ws = kdecay_lib.kdecay_scan_workspace_bytes(B, H, N, D, {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[dt])
-    assert ws == 256 + B * H * -(-N // rows) * D * 8, (ws, rows)
+    assert ws == HDR + B * H * -(-N // rows) * D * 8, (ws, rows)
     g = torch.Generator().manual_seed(180 + B + N % 7)
     lam = lam_uniform(H, 0.5, 0.9999, g)
     V = torch.randn(B, H, N, D, generator=g).to(dt)
