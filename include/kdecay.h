@@ -81,7 +81,7 @@ enum {
  *   workspace    device memory of kdecay_scan_workspace_bytes() bytes,
  *                256-byte aligned, zeroed once by the caller before its first
  *                use.  It holds the look-back words of the chunks and a
- *                header (launch epoch, a completion count, a sticky error
+ *                header (launch epoch, completion counts, a sticky error
  *                word).  Each launch advances the epoch on the device,
  *                so the workspace needs no clearing between launches (also
  *                under stream capture and graph replay), but it must not be
