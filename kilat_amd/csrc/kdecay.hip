@@ -2008,6 +2008,53 @@ ChunkShape chunk_shape(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) 
   return ChunkShape{kR, kNW};
 }
 
+// Batch slices.  Heads of one full 128-byte channel group (bf16/fp16 D=64,
+// fp32 D=32, fp64 D=16), a batch of at least 2, at most kSliceChain chunks
+// of 512 rows per stream and more than one resident round of them
+// (kSliceRound: four 16-row workgroups per CU on 256 CUs) run as that many
+// launches over balanced slices of the batch, each one round at most of
+// 512-row chunks: a launch of several rounds starts its later rounds only as
+// the earlier ones finish, after their rows' full latency, where back-to-back
+// launches overlap one's end with the next one's start.  Measured (bf16 D=64
+// N=4096, same-box A/B, us, one launch / slices): H=12 B=11 27.7 / 26.5 (2),
+// B=12 28.1 / 28.4 (2), B=13 29.9 / 29.6 (2), B=14 33.3 / 30.7 (2), B=16 38.4 / 35.1 (2), B=20 47.2 / 42.5 (2), B=24
+// 57.7 / 52.3 (3), B=32 72.0 / 69.9 (4), B=48 110.4 / 105.6 (6), B=64 142.9 /
+// 140.9 (8); H=16 B=10 32.1 / 30.0, B=12 38.0 / 34.6, B=16 46.5 / 44.2, B=24
+// 71.6 / 66.4, B=40 120.4 / 110.8; N=2048 H=12 B=32 38.4 / 35.0, N=1024
+// H=12 B=64 39.4 / 35.0, N=512 B=128 38.1 / 33.7; fp32 D=32 B=16 H=12 37.7 /
+// 35.2.  Not for longer chains (N=8192 H=12 B=8, 16 per stream: 34.4 /
+// 35.6) and not for heads of several groups, which the six-per-CU grid
+// serves better (fp32 D=64 B=8 H=12 35.0 / 37.1 in two slices, fp64 D=64
+// 70.0 / 75.4 in three).  Of the slice counts from the fewest that fit one
+// round each to two more, the one with the fewest compute-unit rounds in all
+// (n launches of ceil(B / n) batch elements, ceil(chunks / kSliceCUs)
+// workgroups per CU each; ties to fewer launches): whole rounds of three or
+// four workgroups per CU beat more, larger slices that leave CUs a workgroup
+// short (B=64 H=12 in 7 slices of 9-10: 147.7, in 8 of 8: 140.9; B=48 in 5:
+// 107.5, in 6: 105.6), and fewer launches win the ties (B=16 H=16 in 2: 44.2,
+// in 3: 47.2; B=12 H=16 in 2: 34.6, in 3: 40.0).  Returns the number of
+// launches (1: one for the whole batch); slice i holds batch elements
+// [i B / n, (i+1) B / n).
+constexpr int64_t kSliceRound = 1024;
+constexpr int64_t kSliceCUs = 256;
+constexpr int64_t kSliceChain = 8;
+int64_t fwd_slices(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
+  const int64_t DG = group_width(v_dtype, D);
+  if (B < 2 || DG != D || DG * elem_size(v_dtype) != 128) return 1;
+  const int64_t L = chunk_rows(v_dtype, D, ChunkShape{kR, kNW});
+  const int64_t chain = (N + L - 1) / L;
+  const int64_t per_b = H * chain;  // 512-row chunks of one batch element
+  if (chain > kSliceChain || per_b > kSliceRound || B * per_b <= kSliceRound) return 1;
+  const int64_t b_max = kSliceRound / per_b;
+  const int64_t fewest = (B + b_max - 1) / b_max;
+  int64_t best = fewest, best_rounds = 0;
+  for (int64_t n = fewest; n <= fewest + 2 && n <= B; ++n) {
+    const int64_t rounds = n * (((B + n - 1) / n * per_b + kSliceCUs - 1) / kSliceCUs);
+    if (n == fewest || rounds < best_rounds) best = n, best_rounds = rounds;
+  }
+  return best;
+}
+
 // Head dims of the chunked kernels: 16, 32, or any multiple of a full
 // 128-byte channel group (64 bf16/fp16 or 32 fp32 channels); a head is then
 // D / group_width independent streams.  (A group of 16 or 32 channels takes
@@ -2379,10 +2426,13 @@ uint32_t kdecay_debug_fastdiv(uint32_t n, uint32_t d, int want_mod) {
 
 size_t kdecay_scan_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   if (B <= 0 || H <= 0 || N <= 0 || !fwd_dtype_ok(v_dtype) || !head_dim_ok(v_dtype, D)) return 0;
-  const int64_t L = chunk_rows(v_dtype, D, chunk_shape(B, H, N, D, v_dtype));
+  const int64_t n = fwd_slices(B, H, N, D, v_dtype);
+  // Batch slices run one after another on the workspace: the largest one's.
+  const int64_t Bs = (B + n - 1) / n;
+  const int64_t L = chunk_rows(v_dtype, D, n > 1 ? ChunkShape{kR, kNW} : chunk_shape(B, H, N, D, v_dtype));
   const int64_t nchunk = (N + L - 1) / L;
   if (nchunk <= 1) return 0;
-  return kHeaderBytes + (size_t)(B * H * nchunk * D) * sizeof(u64);
+  return kHeaderBytes + (size_t)(Bs * H * nchunk * D) * sizeof(u64);
 }
 
 static int scan_fwd_impl(const void* V, int v_dtype, const int64_t* v_strides, void* out, int out_dtype,
@@ -2408,57 +2458,77 @@ static int scan_fwd_impl(const void* V, int v_dtype, const int64_t* v_strides, v
       return fail(KDECAY_ELAYOUT, "stride %d is not a multiple of 16 bytes", k);
   }
 
-  const ChunkShape shape = chunk_shape(B, H, N, D, v_dtype);
-  const int64_t L = chunk_rows(v_dtype, D, shape);
-  const int64_t nchunk = (N + L - 1) / L;
   const int64_t DG = group_width(v_dtype, D);
-  const int64_t nstream = B * H * (D / DG);
-  const int64_t grid = nchunk * nstream;
-  if (grid > 0x7fffffffLL || nchunk > 0x7fffffffLL || nstream > 0x7fffffffLL)
-    return fail(KDECAY_EINVAL, "problem too large (%lld chunks)", (long long)grid);
+  {
+    const int64_t L = chunk_rows(v_dtype, D, chunk_shape(B, H, N, D, v_dtype));
+    const int64_t nchunk = (N + L - 1) / L, nstream = B * H * (D / DG), grid = nchunk * nstream;
+    if (grid > 0x7fffffffLL || nchunk > 0x7fffffffLL || nstream > 0x7fffffffLL)
+      return fail(KDECAY_EINVAL, "problem too large (%lld chunks)", (long long)grid);
+  }
   const size_t need = kdecay_scan_workspace_bytes(B, H, N, D, v_dtype);
   if (need && (!workspace || workspace_bytes < need))
     return fail(KDECAY_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
   if (need && ((uintptr_t)workspace & 255u)) return fail(KDECAY_EWORKSPACE, "workspace must be 256-byte aligned");
 
-  ScanArgs a;
-  a.V = V;
-  a.out = out;
-  a.lam = lam;
-  a.init = init_state;
-  a.fin = final_state;
-  a.vb = v_strides[0];
-  a.vh = v_strides[1];
-  a.vn = v_strides[2];
-  a.ob = out_strides[0];
-  a.oh = out_strides[1];
-  a.on = out_strides[2];
-  a.H = H;
-  a.N = N;
-  a.t_offset = t_offset;
-  a.D = D;
-  a.ng = (int)(D / DG);
-  a.nchunk = (int)nchunk;
-  a.nstream = (int)nstream;
-  a.f_nstream = make_fastdiv((uint32_t)nstream);
-  a.f_ng = make_fastdiv((uint32_t)a.ng);
-  a.f_H = make_fastdiv((uint32_t)H);
-  a.hdr = need ? static_cast<unsigned*>(workspace) : nullptr;
-  a.spin_limit = spin_limit();
-  a.flags = need ? reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes) : nullptr;
-  a.state_rows = bwd_chunk_rows(B, H, N, D, v_dtype);
-  a.nsaved = (N + a.state_rows - 1) / a.state_rows;
-  a.states = a.nsaved > 1 ? states : nullptr;
-  a.rowtab = a.states ? reinterpret_cast<float2*>(states + B * H * D * a.nsaved) : nullptr;
+  // The training forward's saved states follow the whole batch's backward
+  // chunks, and batch 0's workgroups write the per-row terms once.
+  const int64_t state_rows = bwd_chunk_rows(B, H, N, D, v_dtype);
+  const int64_t nsaved = (N + state_rows - 1) / state_rows;
+  float* const saved = nsaved > 1 ? states : nullptr;
+  float2* const rowtab = saved ? reinterpret_cast<float2*>(saved + B * H * D * nsaved) : nullptr;
+  const int64_t nslice = fwd_slices(B, H, N, D, v_dtype);
+  for (int64_t i = 0; i < nslice; ++i) {
+    const int64_t b0 = B * i / nslice, Bs = B * (i + 1) / nslice - b0;
+    const ChunkShape shape = nslice > 1 ? ChunkShape{kR, kNW} : chunk_shape(B, H, N, D, v_dtype);
+    const int64_t L = chunk_rows(v_dtype, D, shape);
+    const int64_t nchunk = (N + L - 1) / L;
+    const int64_t nstream = Bs * H * (D / DG);
+    const int64_t grid = nchunk * nstream;
+    const bool multi = nchunk > 1;
 
-  if (v_dtype == KDECAY_F32) return dispatch_dg<float, float>(a, DG, grid, s, shape);
-  if (v_dtype == KDECAY_F64) return dispatch_dg<double, double>(a, DG, grid, s, shape);
-  if (v_dtype == KDECAY_BF16) {
-    if (out_dtype == KDECAY_BF16) return dispatch_dg<__bf16, __bf16>(a, DG, grid, s, shape);
-    return dispatch_dg<__bf16, float>(a, DG, grid, s, shape);
+    ScanArgs a;
+    a.V = static_cast<const char*>(V) + b0 * v_strides[0] * elem_size(v_dtype);
+    a.out = static_cast<char*>(out) + b0 * out_strides[0] * elem_size(out_dtype);
+    a.lam = lam;
+    a.init = init_state ? init_state + b0 * H * D : nullptr;
+    a.fin = final_state ? final_state + b0 * H * D : nullptr;
+    a.vb = v_strides[0];
+    a.vh = v_strides[1];
+    a.vn = v_strides[2];
+    a.ob = out_strides[0];
+    a.oh = out_strides[1];
+    a.on = out_strides[2];
+    a.H = H;
+    a.N = N;
+    a.t_offset = t_offset;
+    a.D = D;
+    a.ng = (int)(D / DG);
+    a.nchunk = (int)nchunk;
+    a.nstream = (int)nstream;
+    a.f_nstream = make_fastdiv((uint32_t)nstream);
+    a.f_ng = make_fastdiv((uint32_t)a.ng);
+    a.f_H = make_fastdiv((uint32_t)H);
+    a.hdr = multi ? static_cast<unsigned*>(workspace) : nullptr;
+    a.spin_limit = spin_limit();
+    a.flags = multi ? reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes) : nullptr;
+    a.state_rows = state_rows;
+    a.nsaved = nsaved;
+    a.states = saved ? saved + b0 * H * D * nsaved : nullptr;
+    a.rowtab = i == 0 ? rowtab : nullptr;
+
+    if (v_dtype == KDECAY_F32)
+      rc = dispatch_dg<float, float>(a, DG, grid, s, shape);
+    else if (v_dtype == KDECAY_F64)
+      rc = dispatch_dg<double, double>(a, DG, grid, s, shape);
+    else if (v_dtype == KDECAY_BF16)
+      rc = out_dtype == KDECAY_BF16 ? dispatch_dg<__bf16, __bf16>(a, DG, grid, s, shape)
+                                    : dispatch_dg<__bf16, float>(a, DG, grid, s, shape);
+    else
+      rc = out_dtype == KDECAY_F16 ? dispatch_dg<_Float16, _Float16>(a, DG, grid, s, shape)
+                                   : dispatch_dg<_Float16, float>(a, DG, grid, s, shape);
+    if (rc) return rc;
   }
-  if (out_dtype == KDECAY_F16) return dispatch_dg<_Float16, _Float16>(a, DG, grid, s, shape);
-  return dispatch_dg<_Float16, float>(a, DG, grid, s, shape);
+  return 0;
 }
 
 int kdecay_scan_fwd(const void* V, int v_dtype, const int64_t* v_strides, void* out, int out_dtype,

@@ -82,13 +82,28 @@ def test_workspace_bytes(kdecay_lib):
     assert ws(10, 16, 512, 64, _lib.KDECAY_BF16) == HDR + 10 * 16 * 2 * 64 * 8  # 160, 1 per stream: 8 rows
     assert ws(11, 16, 512, 64, _lib.KDECAY_BF16) == 0  # 176 single-chunk streams: 16 rows, no look-back
     assert ws(2, 6, 1024, 48, _lib.KDECAY_BF16) == 0  # unsupported D
-    # Just above one resident round of 512-row chunks (8 or fewer per stream, full
-    # 128-byte groups): 256-row chunks, six workgroups per compute unit.
-    assert ws(13, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 13 * 12 * 8 * 64 * 8  # 1248: 16 rows
-    assert ws(14, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 14 * 12 * 16 * 64 * 8  # 1344: 8 rows
-    assert ws(16, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 16 * 12 * 16 * 64 * 8  # 1536: 8 rows
-    assert ws(17, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 17 * 12 * 8 * 64 * 8  # 1632: 16 rows
-    assert ws(14, 12, 4097, 64, _lib.KDECAY_BF16) == HDR + 14 * 12 * 9 * 64 * 8  # 9 per stream: 16 rows
+    # Heads of one full 128-byte group, B >= 2, at most 8 chunks of 512 rows per
+    # stream and more than 1024 of them: balanced batch slices of at most 1024
+    # chunks, one launch each, one after another on the workspace (the largest
+    # slice's words); 512-row chunks.
+    assert ws(10, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 10 * 12 * 8 * 64 * 8  # 960: one launch
+    assert ws(11, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 6 * 12 * 8 * 64 * 8  # 1056: slices of 5 and 6
+    assert ws(13, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 7 * 12 * 8 * 64 * 8  # 1248: 6 + 7
+    assert ws(16, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 8 * 12 * 8 * 64 * 8  # 1536: 8 + 8
+    assert ws(17, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 9 * 12 * 8 * 64 * 8  # 1632: 8 + 9
+    assert ws(64, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 8 * 12 * 8 * 64 * 8  # 8 slices of 768 chunks, not 7 of 864-960
+    assert ws(20, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 10 * 12 * 8 * 64 * 8  # 2 of 960 (4 per CU), not 4 of 480
+    assert ws(40, 16, 4096, 64, _lib.KDECAY_BF16) == HDR + 8 * 16 * 8 * 64 * 8  # 5 of 1024
+    assert ws(16, 12, 4096, 32, _lib.KDECAY_F32) == HDR + 8 * 12 * 8 * 32 * 8  # fp32 D=32: 8 + 8
+    assert ws(128, 12, 512, 64, _lib.KDECAY_BF16) == 0  # 2 slices of single-chunk streams
+    assert ws(14, 12, 4097, 64, _lib.KDECAY_BF16) == HDR + 14 * 12 * 9 * 64 * 8  # 9 per stream: one launch
+    assert ws(3, 12, 8192, 64, _lib.KDECAY_BF16) == HDR + 3 * 12 * 16 * 64 * 8  # 16 per stream: one launch
+    # At B=1, just above one resident round of 512-row chunks (8 or fewer per
+    # stream, full 128-byte groups): 256-row chunks, six workgroups per compute unit.
+    assert ws(1, 156, 4096, 64, _lib.KDECAY_BF16) == HDR + 156 * 8 * 64 * 8  # 1248: 16 rows
+    assert ws(1, 168, 4096, 64, _lib.KDECAY_BF16) == HDR + 168 * 16 * 64 * 8  # 1344: 8 rows
+    assert ws(1, 192, 4096, 64, _lib.KDECAY_BF16) == HDR + 192 * 16 * 64 * 8  # 1536: 8 rows
+    assert ws(1, 204, 4096, 64, _lib.KDECAY_BF16) == HDR + 204 * 8 * 64 * 8  # 1632: 16 rows
     assert ws(5, 12, 4096, 128, _lib.KDECAY_BF16) == HDR + 5 * 12 * 8 * 128 * 8  # 960 in 2 groups: one round, 16 rows
     assert ws(6, 12, 4096, 128, _lib.KDECAY_BF16) == HDR + 6 * 12 * 16 * 128 * 8  # 1152 in 2 groups: 8 rows
     assert ws(8, 12, 4096, 64, _lib.KDECAY_F32) == HDR + 8 * 12 * 16 * 64 * 8  # 1536 in 2 groups: 8 rows

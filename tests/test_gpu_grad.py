@@ -618,6 +618,25 @@ def test_backward_after_training_forward_of_many_streams(hip_device, kdecay_lib)
         check(dv, dl, di, rdv, rdl, rdi, torch.bfloat16, f"rep {rep} B={B} H={H} N={N} D={D}")
 
 
+@pytest.mark.parametrize("B,H,N,dname", [(11, 12, 4096, "bf16"), (43, 12, 1024, "bf16")])
+def test_backward_after_batch_sliced_training_forward(hip_device, kdecay_lib, B, H, N, dname):
+    """A training forward that runs as two batch slices (more than 1024
+    chunks of 512 rows of one-group heads) saves each slice's states where
+    the whole batch's backward reads them, and the first slice alone writes
+    the per-row terms; against the oracle's float64 adjoint, with carry-in,
+    final-state gradient and offset."""
+    dtype = DTYPES[dname]
+    g = torch.Generator().manual_seed(740 + B)
+    lam = lam_uniform(H, 0.5, 0.999, g)
+    V = torch.randn(B, H, N, 64, generator=g).to(dtype)
+    gy = torch.randn(B, H, N, 64, generator=g).to(dtype)
+    init = torch.randn(B, H, 64, generator=g)
+    gfin = torch.randn(B, H, 64, generator=g)
+    dv, dl, di = gpu_grads(lam, V, gy, hip_device, init=init, gfin=gfin, t_offset=21)
+    rdv, rdl, rdi = O.scan_grads_f64(lam, V, gy, init_state=init, gfin=gfin, t_offset=21)
+    check(dv, dl, di, rdv, rdl, rdi, dtype, f"{dname} B={B} H={H} N={N}")
+
+
 @pytest.mark.parametrize("B,H,N,D,dname", [(8, 12, 2048, 64, "bf16"), (1, 16, 8192, 64, "bf16"),
                                            (4, 12, 2048, 64, "f32")])
 def test_backward_one_round_of_256_row_chunks(hip_device, kdecay_lib, B, H, N, D, dname):

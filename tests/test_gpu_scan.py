@@ -231,16 +231,17 @@ def test_chunk_size_switch_short_chains(hip_device, kdecay_lib, B, N, nchunk):
 
 
 @pytest.mark.parametrize("dname,B,H,N,D,six", [
-    ("bf16", 13, 12, 4096, 64, False),  # 1248 chunks of 512 rows: 16 rows per lane, 2 rounds
-    ("bf16", 14, 12, 4096, 64, True),   # 1344: 256-row chunks, six workgroups per CU
-    ("bf16", 16, 12, 4096, 64, True),   # 1536
-    ("bf16", 17, 12, 4096, 64, False),  # 1632
-    ("bf16", 14, 12, 4097, 64, False),  # 9 chunks per stream
-    ("bf16", 28, 12, 2048, 64, True),   # 4 chunks per stream
+    # one 128-byte group per head at B=1 (larger batches run as batch slices)
+    ("bf16", 1, 156, 4096, 64, False),  # 1248 chunks of 512 rows: 16 rows per lane, 2 rounds
+    ("bf16", 1, 168, 4096, 64, True),   # 1344: 256-row chunks, six workgroups per CU
+    ("bf16", 1, 192, 4096, 64, True),   # 1536
+    ("bf16", 1, 204, 4096, 64, False),  # 1632
+    ("bf16", 1, 168, 4097, 64, False),  # 9 chunks per stream
+    ("bf16", 1, 336, 2048, 64, True),   # 4 chunks per stream
     ("bf16", 5, 12, 4096, 128, False),  # 960 in two channel groups per head: one round
     ("bf16", 6, 12, 4096, 128, True),   # 1152
     ("f32", 8, 12, 4096, 64, True),     # 1536 in two groups of 32 fp32 channels
-    ("f16", 16, 12, 4096, 64, True),
+    ("f16", 1, 192, 4096, 64, True),
     # heads of four or more groups: 256-row chunks from 1024 chunks of 512 rows up, 32 or fewer per stream
     ("bf16", 2, 12, 4096, 256, False),  # 768: below a full round
     ("bf16", 4, 8, 4096, 256, True),    # 1024
@@ -273,6 +274,43 @@ def test_chunk_shape_just_above_one_round(hip_device, kdecay_lib, dname, B, H, N
     if dt == torch.bfloat16 and es == 2:
         y32 = gpu_scan(lam, V, hip_device, initial_state=init.to(hip_device), t_offset=5, out_dtype=torch.float32)
         assert_parity(y32, ref32, torch.float32, f"{dname} fp32 out")
+        assert torch.equal(y32.to(dt), y)
+
+
+@pytest.mark.parametrize("dname,B,H,N,D,nslice", [
+    ("bf16", 10, 12, 4096, 64, 1),   # 960 chunks of 512 rows: one launch
+    ("bf16", 11, 12, 4096, 64, 2),   # 1056: batch slices of 5 and 6
+    ("bf16", 17, 12, 4096, 64, 2),   # 8 + 9
+    ("bf16", 48, 12, 4096, 64, 6),   # six slices of 768 chunks
+    ("f16", 12, 16, 4096, 64, 2),
+    ("f32", 16, 12, 4096, 32, 2),    # one 128-byte group of fp32
+    ("bf16", 43, 12, 1024, 64, 2),   # 2 chunks per stream
+    ("bf16", 128, 12, 512, 64, 2),   # single-chunk streams: no look-back
+    ("bf16", 9, 12, 8192, 64, 1),    # 16 chunks per stream: one launch
+])
+def test_batch_slices(hip_device, kdecay_lib, dname, B, H, N, D, nslice):
+    """Heads of one full 128-byte channel group, with at most 8 chunks of 512
+    rows per stream and more than 1024 of them, run as launches over balanced
+    slices of the batch, one after another on the workspace (sized for the
+    largest slice); against the oracle with a carried state, an offset and
+    the final state, and for bf16 also the fp32 output."""
+    dt = DTYPES[dname]
+    rows = chunk_rows(dt, D, 16)
+    chain = -(-N // rows)
+    ws = kdecay_lib.kdecay_scan_workspace_bytes(B, H, N, D, {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[dt])
+    assert ws == (HDR + -(-B // nslice) * H * chain * D * 8 if chain > 1 else 0), ws
+    g = torch.Generator().manual_seed(230 + B + N % 7)
+    lam = lam_uniform(H, 0.5, 0.9999, g)
+    V = torch.randn(B, H, N, D, generator=g).to(dt)
+    init = torch.randn(B, H, D, generator=g)
+    y, fin = gpu_scan(lam, V, hip_device, initial_state=init.to(hip_device), return_final_state=True, t_offset=9)
+    ref, sref = C.scan_f32(lam.numpy(), V.float().numpy(), init.numpy(), 9)
+    ref32 = torch.from_numpy(ref)
+    assert_parity(y.cpu(), ref32.to(dt), dt, f"{dname} B={B} H={H} N={N}")
+    assert rel_err(fin.cpu(), torch.from_numpy(sref)) <= 1e-5
+    if dt == torch.bfloat16:
+        y32 = gpu_scan(lam, V, hip_device, initial_state=init.to(hip_device), t_offset=9, out_dtype=torch.float32)
+        assert_parity(y32.cpu(), ref32, torch.float32, f"{dname} fp32 out")
         assert torch.equal(y32.to(dt), y)
 
 
