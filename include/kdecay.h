@@ -78,6 +78,11 @@ enum {
  *                with in a Python loop (attention.py:383-394, :722-727).
  *   t_offset     absolute position of row 0 (enters z only); 0 for a whole
  *                sequence.
+ *   stream       the HIP stream the work goes to: one kernel launch, or for
+ *                heads of one 128-byte channel group with more than one
+ *                resident round of short streams, a few launches over
+ *                slices of the batch, in order on this stream (also under
+ *                stream capture).
  *   workspace    device memory of kdecay_scan_workspace_bytes() bytes,
  *                256-byte aligned, zeroed once by the caller before its first
  *                use.  It holds the look-back words of the chunks and a
