@@ -383,6 +383,43 @@ def bench_forward_dtypes(torch, dev, steps=100):
     return out
 
 
+def bench_forward_grids(torch, dev, steps=50):
+    """bf16 D=64 N=4096 grids of more than one resident round of 512-row
+    chunks, which the library runs as batch slices of whole CU rounds: B=16
+    and B=24 at H=12 (two and three launches of 768 chunks) and the larger
+    sample configuration's decay heads (H=16 of 64 channels) at B=12 (two
+    launches of 768).  Algorithmic bytes: V read once, y written once; 4
+    rotated sets carved from one allocation."""
+    from kilat_amd import _lib
+    from kilat_amd.triton_ops import _stream_ptr, _workspace
+
+    N, D = 4096, 64
+    lib = _lib.load()
+    code = _lib.KDECAY_BF16
+    stream = _stream_ptr(dev)
+    out = {}
+    for name, B, H in (("B16_H12", 16, 12), ("B24_H12", 24, 12), ("B12_H16", 12, 16)):
+        lam = c2_lam(H, torch).to(dev)
+        sets = carved_pairs(torch, dev, (B, H, N, D), torch.bfloat16, torch.bfloat16, 4, seed=13)
+        ws = _workspace(dev, stream, lib.kdecay_scan_workspace_bytes(B, H, N, D, code))
+        args = [(V.data_ptr(), code, _lib.strides4(V.stride()), y.data_ptr(), code, _lib.strides4(y.stride()),
+                 lam.data_ptr(), None, None, B, H, N, D, 0, ws.data_ptr(), ws.numel(), stream) for V, y in sets]
+        rc = [0]
+
+        def launch(k, args=args, rc=rc):
+            rc[0] |= lib.kdecay_scan_fwd(*args[k % len(args)])
+
+        region, _ = time_region(torch, launch, steps, 100, events=False, warm_ms=EXTRA_WARM_MS)
+        if rc[0]:
+            raise RuntimeError("scan failed: " + lib.kdecay_last_error_string().decode())
+        us = region * 1e3 / steps
+        nbytes = B * H * N * D * 4
+        out[name] = {"B": B, "H": H, "us": round(us, 3), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "pct_of_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 2)}
+        del sets, args
+    return out
+
+
 def bench_backward(torch, dev, steps=100):
     """C2-shaped training pass: kdecay_scan_fwd_train, then kdecay_scan_bwd (dV, dlam).
 
@@ -760,6 +797,9 @@ def main() -> int:
         torch.cuda.empty_cache()
         log("forward with other I/O types (C2 shape)")
         extras["forward_dtypes"] = bench_forward_dtypes(torch, dev)
+        torch.cuda.empty_cache()
+        log("forward, grids of more than one round (bf16 D=64 N=4096)")
+        extras["forward_grids"] = bench_forward_grids(torch, dev)
         torch.cuda.empty_cache()
         log("end-to-end model forward (C5)")
         extras["e2e"] = bench_e2e(torch, dev)
