@@ -1063,6 +1063,10 @@ struct BwdArgs {
   int ndone;       // workgroups that count toward the epoch's advance (ChunkBwd::run)
   int per_stream;  // 1: the first chunk of every stream counts instead
   FastDiv f_nstream, f_ng, f_H, f_nchunk;  // division by nstream, ng, H and nchunk
+  // Batch slices (kdecay_scan_bwd): this launch is slice `slice` of `nslice`;
+  // the earlier slices' per-head dlam sums, in double ([nslice - 1][H]).
+  int slice, nslice;
+  double* dlam_slices;
 };
 
 // XCDs of the device: workgroups are handed to them round-robin by index, and
@@ -1640,7 +1644,17 @@ struct ChunkBwd {
     }
     acc = wave_sum_f64(acc);
     if (lane == 0) {
-      a.dlam[h] = (float)acc;
+      if (a.slice + 1 < a.nslice) {
+        a.dlam_slices[(int64_t)a.slice * a.H + h] = acc;  // the last slice adds it
+      } else {
+        double t = acc;
+        if (a.slice > 0) {  // the earlier slices' sums in slice order, then this one's
+          t = a.dlam_slices[h];
+          for (int sl = 1; sl < a.slice; ++sl) t += a.dlam_slices[(int64_t)sl * a.H + h];
+          t += acc;
+        }
+        a.dlam[h] = (float)t;
+      }
       if (!a.per_stream && !poisoned) count_done(a.hdr, (unsigned)a.ndone, epoch);
     }
   }
@@ -2585,14 +2599,38 @@ int kdecay_scan_fwd_train(const void* V, int v_dtype, const int64_t* v_strides, 
                        t_offset, workspace, workspace_bytes, states, stream);
 }
 
+// Backward batch slices.  Heads of one full 128-byte channel group on 512-row
+// chunks, at most kSliceChain per stream, whose grid is exactly two or three
+// resident rounds (kBwdOneRound chunks each) divided evenly by the batch: one
+// launch per round-sized slice of the batch, in order on the stream, each
+// slice's dlam sums kept in double in the workspace and added, in slice
+// order, by the last slice.  Measured (bf16 D=64 N=4096, same-box, us, one
+// launch / slices): H=12 B=16 59.25 / 55.28 (2), B=24 88.0 / 83.3 (3); H=16
+// B=12 59.8 / 55.9 (2).  Not in other slicings: slices of part of a round
+// (B=20 H=12 in 2: 72.5 / 75.0; B=12 H=12 in 2: 44.7 / 51.0) or four rounds
+// (B=32 H=12 in 4: 109.2 / 112.0).  Returns the number of launches.
+int64_t bwd_slices(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
+  const int64_t DG = bwd_group_width(B, H, N, D, v_dtype);
+  if (B < 2 || DG != D || DG * elem_size(v_dtype) != 128 || bwd_rows_per_lane(B, H, N, D, v_dtype) != kRB) return 1;
+  const int64_t chain = (N + bwd_chunk_rows(B, H, N, D, v_dtype) - 1) / bwd_chunk_rows(B, H, N, D, v_dtype);
+  const int64_t grid = B * H * chain;
+  if (chain > kSliceChain) return 1;
+  for (int64_t n = 2; n <= 3; ++n)
+    if (B % n == 0 && grid == n * kBwdOneRound) return n;
+  return 1;
+}
+
 size_t kdecay_scan_bwd_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   if (B <= 0 || H <= 0 || N <= 0 || !dtype_ok(v_dtype) || !head_dim_ok(v_dtype, D)) return 0;
+  const int64_t n = bwd_slices(B, H, N, D, v_dtype);
+  const int64_t Bs = B / n;  // slices run one after another on the workspace
   const int64_t Lb = bwd_chunk_rows(B, H, N, D, v_dtype);
   const int64_t nchunk = (N + Lb - 1) / Lb;
-  const size_t flags = nchunk > 1 ? (size_t)(B * H * nchunk * D) * sizeof(u64) : 0;
-  const int64_t nstream = B * H * (D / bwd_group_width(B, H, N, D, v_dtype));
+  const size_t flags = nchunk > 1 ? (size_t)(Bs * H * nchunk * D) * sizeof(u64) : 0;
+  const int64_t nstream = Bs * H * (D / bwd_group_width(B, H, N, D, v_dtype));
   const size_t partial = ((size_t)(nstream * nchunk) * sizeof(u64) + 255) & ~(size_t)255;
-  return kHeaderBytes + flags + partial;
+  const size_t sums = n > 1 ? ((size_t)((n - 1) * H) * sizeof(double) + 255) & ~(size_t)255 : 0;
+  return kHeaderBytes + flags + partial + sums;
 }
 
 int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides, const void* gy,
@@ -2645,64 +2683,77 @@ int kdecay_scan_bwd(const void* V, int v_dtype, const int64_t* v_strides, const 
     return fail(KDECAY_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
   if ((uintptr_t)workspace & 255u) return fail(KDECAY_EWORKSPACE, "workspace must be 256-byte aligned");
 
-  BwdArgs a;
-  a.V = V;
-  a.gy = gy;
-  a.dv = dV;
-  a.lam = lam;
-  a.init = init_state;
-  a.states = states;
-  a.gfin = g_final;
-  a.dinit = d_init;
-  a.dlam = dlam;
-  a.vb = v_strides[0];
-  a.vh = v_strides[1];
-  a.vn = v_strides[2];
-  a.gb = gy_strides[0];
-  a.gh = gy_strides[1];
-  a.gn = gy_strides[2];
-  a.db = dv_strides[0];
-  a.dh = dv_strides[1];
-  a.dn = dv_strides[2];
-  a.B = B;
-  a.H = H;
-  a.N = N;
-  a.t_offset = t_offset;
-  a.D = D;
-  a.ng = (int)(D / DG);
-  a.nchunk = (int)nchunk;
-  a.nstream = (int)nstream;
-  a.nsaved = nchunk;
-  a.rowtab = nchunk > 1 ? reinterpret_cast<const float2*>(states + B * H * D * nchunk) : nullptr;
-  a.f_nstream = make_fastdiv((uint32_t)nstream);
-  a.f_ng = make_fastdiv((uint32_t)a.ng);
-  a.f_H = make_fastdiv((uint32_t)H);
-  a.f_nchunk = make_fastdiv((uint32_t)nchunk);
-  a.hdr = static_cast<unsigned*>(workspace);
-  a.spin_limit = spin_limit();
-  // Workgroups that count toward the epoch's advance: the H that sum a
-  // head's partials (the last row of items, chunk 0, is unrotated: item
-  // (nchunk-1)*nstream + stream with b = B-1 and the last channel group) and
-  // the last of each XCD, each counted once.
-  a.per_stream = nstream <= kBwdPerStreamCount;
-  a.ndone = (int)H;
-  for (int64_t item = grid > kXcds ? grid - kXcds : 0; item < grid; ++item) {
-    const int64_t rc = item / nstream, stream = item - rc * nstream;
-    const int64_t bh = stream / a.ng, grp = stream - bh * a.ng;
-    const bool sums = rc == nchunk - 1 && bh / H == B - 1 && grp == a.ng - 1;
-    if (!sums) ++a.ndone;
+  // Batch slices (bwd_slices): the saved states keep the whole batch's
+  // layout (nchunk per stream, then the per-row terms after all of them).
+  const int64_t nslice = bwd_slices(B, H, N, D, v_dtype);
+  const int64_t Bs = B / nslice;
+  const int64_t nstream_s = Bs * H * (D / DG), grid_s = nchunk * nstream_s;
+  const size_t flag_bytes = nchunk > 1 ? (size_t)(Bs * H * nchunk * D) * sizeof(u64) : 0;
+  const size_t partial_bytes = ((size_t)(nstream_s * nchunk) * sizeof(u64) + 255) & ~(size_t)255;
+  for (int64_t i = 0; i < nslice; ++i) {
+    const int64_t b0 = i * Bs;
+    BwdArgs a;
+    a.V = static_cast<const char*>(V) + b0 * v_strides[0] * es;
+    a.gy = static_cast<const char*>(gy) + b0 * gy_strides[0] * es;
+    a.dv = static_cast<char*>(dV) + b0 * dv_strides[0] * es;
+    a.lam = lam;
+    a.init = init_state ? init_state + b0 * H * D : nullptr;
+    a.states = states ? states + b0 * H * D * nchunk : nullptr;
+    a.gfin = g_final ? g_final + b0 * H * D : nullptr;
+    a.dinit = d_init ? d_init + b0 * H * D : nullptr;
+    a.dlam = dlam;
+    a.vb = v_strides[0];
+    a.vh = v_strides[1];
+    a.vn = v_strides[2];
+    a.gb = gy_strides[0];
+    a.gh = gy_strides[1];
+    a.gn = gy_strides[2];
+    a.db = dv_strides[0];
+    a.dh = dv_strides[1];
+    a.dn = dv_strides[2];
+    a.B = Bs;
+    a.H = H;
+    a.N = N;
+    a.t_offset = t_offset;
+    a.D = D;
+    a.ng = (int)(D / DG);
+    a.nchunk = (int)nchunk;
+    a.nstream = (int)nstream_s;
+    a.nsaved = nchunk;
+    a.rowtab = nchunk > 1 ? reinterpret_cast<const float2*>(states + B * H * D * nchunk) : nullptr;
+    a.f_nstream = make_fastdiv((uint32_t)nstream_s);
+    a.f_ng = make_fastdiv((uint32_t)a.ng);
+    a.f_H = make_fastdiv((uint32_t)H);
+    a.f_nchunk = make_fastdiv((uint32_t)nchunk);
+    a.hdr = static_cast<unsigned*>(workspace);
+    a.spin_limit = spin_limit();
+    // Workgroups that count toward the epoch's advance: the H that sum a
+    // head's partials (the last row of items, chunk 0, is unrotated: item
+    // (nchunk-1)*nstream + stream with b = B-1 and the last channel group) and
+    // the last of each XCD, each counted once.
+    a.per_stream = nstream_s <= kBwdPerStreamCount;
+    a.ndone = (int)H;
+    for (int64_t item = grid_s > kXcds ? grid_s - kXcds : 0; item < grid_s; ++item) {
+      const int64_t rc = item / nstream_s, stream = item - rc * nstream_s;
+      const int64_t bh = stream / a.ng, grp = stream - bh * a.ng;
+      const bool sums = rc == nchunk - 1 && bh / H == Bs - 1 && grp == a.ng - 1;
+      if (!sums) ++a.ndone;
+    }
+    a.flags = nchunk > 1 ? reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes) : nullptr;
+    a.partial = reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes + flag_bytes);
+    a.slice = (int)i;
+    a.nslice = (int)nslice;
+    a.dlam_slices = reinterpret_cast<double*>(static_cast<char*>(workspace) + kHeaderBytes + flag_bytes + partial_bytes);
+    int e;
+    if (v_dtype == KDECAY_F32)
+      e = dispatch_bwd<float>(a, DG, grid_s, RB, s);
+    else if (v_dtype == KDECAY_BF16)
+      e = dispatch_bwd<__bf16>(a, DG, grid_s, RB, s);
+    else
+      e = dispatch_bwd<_Float16>(a, DG, grid_s, RB, s);
+    if (e) return e;
   }
-  const size_t flag_bytes = nchunk > 1 ? (size_t)(B * H * nchunk * D) * sizeof(u64) : 0;
-  a.flags = nchunk > 1 ? reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes) : nullptr;
-  a.partial = reinterpret_cast<u64*>(static_cast<char*>(workspace) + kHeaderBytes + flag_bytes);
-  int e;
-  if (v_dtype == KDECAY_F32)
-    e = dispatch_bwd<float>(a, DG, grid, RB, s);
-  else if (v_dtype == KDECAY_BF16)
-    e = dispatch_bwd<__bf16>(a, DG, grid, RB, s);
-  else
-    e = dispatch_bwd<_Float16>(a, DG, grid, RB, s);
-  return e;
+  return 0;
 }
 
 int kdecay_scan_fwd_sequential(const void* V, int v_dtype, const int64_t* v_strides, void* out,

@@ -167,6 +167,20 @@ def test_backward_workspace_bytes(kdecay_lib):
     assert wb(12, 12, 4096, 32, _lib.KDECAY_F32) == words(12, 12, 4096, 32, 144, 8)  # one group: 512 rows
     assert wb(2, 16, 32768, 128, _lib.KDECAY_BF16) == words(2, 16, 32768, 128, 64, 128)  # 64 streams of 128 B
     assert wb(1, 16, 65536, 128, _lib.KDECAY_F32) == words(1, 16, 65536, 128, 64, 256)  # four groups of 32 fp32
+    # one-group heads on 512-row chunks, at most 8 per stream, in exactly two or three
+    # resident rounds (768 chunks each) that the batch divides evenly: one launch per
+    # round-sized batch slice, one after another on the workspace (one slice's words),
+    # and the earlier slices' dlam sums in double (256-byte aligned)
+    sums = lambda n, H: ((n - 1) * H * 8 + 255) // 256 * 256
+    assert wb(16, 12, 4096, 64, _lib.KDECAY_BF16) == words(8, 12, 4096, 64, 96, 8) + sums(2, 12)  # 2 x 768
+    assert wb(24, 12, 4096, 64, _lib.KDECAY_BF16) == words(8, 12, 4096, 64, 96, 8) + sums(3, 12)  # 3 x 768
+    assert wb(12, 16, 4096, 64, _lib.KDECAY_F16) == words(6, 16, 4096, 64, 96, 8) + sums(2, 16)
+    assert wb(96, 12, 1024, 64, _lib.KDECAY_BF16) == words(32, 12, 1024, 64, 384, 2) + sums(3, 12)  # chains of 2
+    assert wb(16, 12, 4096, 32, _lib.KDECAY_F32) == words(8, 12, 4096, 32, 96, 8) + sums(2, 12)  # fp32 D=32
+    assert wb(20, 12, 4096, 64, _lib.KDECAY_BF16) == words(20, 12, 4096, 64, 240, 8)  # 1920: one launch
+    assert wb(32, 12, 4096, 64, _lib.KDECAY_BF16) == words(32, 12, 4096, 64, 384, 8)  # four rounds: one launch
+    assert wb(16, 12, 4097, 64, _lib.KDECAY_BF16) == words(16, 12, 4097, 64, 192, 9)  # 9 per stream: one launch
+    assert wb(2, 6, 65536, 64, _lib.KDECAY_BF16) == words(2, 6, 65536, 64, 12, 128)  # 1536 in chains of 128: one
 
 
 def test_saved_states_floats(kdecay_lib):

@@ -637,6 +637,58 @@ def test_backward_after_batch_sliced_training_forward(hip_device, kdecay_lib, B,
     check(dv, dl, di, rdv, rdl, rdi, dtype, f"{dname} B={B} H={H} N={N}")
 
 
+def test_backward_in_two_batch_slices_matches_oracle(hip_device, kdecay_lib):
+    """One-group heads whose backward grid is exactly two resident rounds
+    (B=16 H=12 N=4096: 2 x 768 chunks of 512 rows) run as two launches over
+    halves of the batch, the second adding the first one's dlam sums in
+    double; against the oracle's float64 adjoint, with carry-in, final-state
+    gradient and offset."""
+    B, H, N, D = 16, 12, 4096, 64
+    assert _lib.load().kdecay_scan_bwd_workspace_bytes(B, H, N, D, _lib.KDECAY_BF16) > \
+        _lib.load().kdecay_scan_bwd_workspace_bytes(B // 2, H, N, D, _lib.KDECAY_BF16)
+    g = torch.Generator().manual_seed(760)
+    lam = lam_uniform(H, 0.5, 0.999, g)
+    V = torch.randn(B, H, N, D, generator=g).to(torch.bfloat16)
+    gy = torch.randn(B, H, N, D, generator=g).to(torch.bfloat16)
+    init = torch.randn(B, H, D, generator=g)
+    gfin = torch.randn(B, H, D, generator=g)
+    dv, dl, di = gpu_grads(lam, V, gy, hip_device, init=init, gfin=gfin, t_offset=3)
+    rdv, rdl, rdi = O.scan_grads_f64(lam, V, gy, init_state=init, gfin=gfin, t_offset=3)
+    check(dv, dl, di, rdv, rdl, rdi, torch.bfloat16, f"B={B} H={H} N={N}")
+
+
+def test_backward_batch_slices_equal_separate_launches(hip_device, kdecay_lib):
+    """B=24 H=12 N=4096 (3 x 768 chunks) runs as three backward launches of 8
+    batch elements each: dV and d(init) bit for bit those of three separate
+    training passes over the same thirds of the batch (each one launch of 768
+    chunks), and dlam their sum, to the parts' fp32 rounding."""
+    B, H, N, D = 24, 12, 4096, 64
+    g = torch.Generator(device=hip_device).manual_seed(770)
+    lam = (0.5 + 0.499 * torch.rand(H, generator=g, device=hip_device)).float()
+    V = torch.randn(B, H, N, D, generator=g, device=hip_device).to(torch.bfloat16)
+    gy = torch.randn(B, H, N, D, generator=g, device=hip_device).to(torch.bfloat16)
+    init = torch.randn(B, H, D, generator=g, device=hip_device)
+    gfin = torch.randn(B, H, D, generator=g, device=hip_device)
+
+    def grads(b0, b1):
+        lam_d = lam.clone().requires_grad_(True)
+        V_d = V[b0:b1].clone().requires_grad_(True)
+        i_d = init[b0:b1].clone().requires_grad_(True)
+        y, fin = kilat_amd.global_decay_scan(lam_d, V_d, initial_state=i_d, return_final_state=True, t_offset=7)
+        ((y.float() * gy[b0:b1].float()).sum() + (fin * gfin[b0:b1]).sum()).backward()
+        torch.cuda.synchronize()
+        return V_d.grad, lam_d.grad.double(), i_d.grad
+
+    print("  grad V(24, 12, 4096, 64) in three slices, then three separate thirds", flush=True)
+    dv, dl, di = grads(0, B)
+    parts = [grads(b0, b0 + 8) for b0 in (0, 8, 16)]
+    assert torch.equal(dv, torch.cat([p[0] for p in parts]))
+    assert torch.equal(di, torch.cat([p[2] for p in parts]))
+    dl_sum = parts[0][1] + parts[1][1] + parts[2][1]
+    scale = parts[0][1].abs() + parts[1][1].abs() + parts[2][1].abs()  # each part is rounded to fp32 once
+    assert bool(((dl.double() - dl_sum).abs() <= 1e-6 * scale).all()), (dl, dl_sum)
+
+
 @pytest.mark.parametrize("B,H,N,D,dname", [(8, 12, 2048, 64, "bf16"), (1, 16, 8192, 64, "bf16"),
                                            (4, 12, 2048, 64, "f32")])
 def test_backward_one_round_of_256_row_chunks(hip_device, kdecay_lib, B, H, N, D, dname):
