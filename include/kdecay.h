@@ -235,7 +235,11 @@ size_t kdecay_scan_saved_states_floats(int64_t B, int64_t H, int64_t N,
  *                kdecay_scan_saved_states_floats() is 0)
  *   g_final      nullable fp32 [B,H,D]: gradient of the forward's final state
  *   dlam         fp32 [H], overwritten (summed over B, D and t in a fixed
- *                order: deterministic)
+ *                order: deterministic).  One-group heads whose grid is exactly
+ *                two or three resident rounds run as that many launches over
+ *                slices of the batch, in order on `stream`; the last adds
+ *                the earlier slices' sums (kept in double in the workspace)
+ *                in slice order, so dlam is still one value per head.
  *   d_init       nullable fp32 [B,H,D]
  *   workspace    kdecay_scan_bwd_workspace_bytes() bytes, 256-byte aligned,
  *                zeroed once; same rules as kdecay_scan_fwd's (it may be the
