@@ -2048,10 +2048,16 @@ ChunkShape chunk_shape(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) 
 // 107.5, in 6: 105.6), and fewer launches win the ties (B=16 H=16 in 2: 44.2,
 // in 3: 47.2; B=12 H=16 in 2: 34.6, in 3: 40.0).  Returns the number of
 // launches (1: one for the whole batch); slice i holds batch elements
-// [i B / n, (i+1) B / n).
+// [i B / n, (i+1) B / n).  At most kSliceMax launches, the range measured
+// (each adds a launch's fixed cost): grids that need more run as one.  A grid
+// of four rounds or more, whose one launch already spreads its round changes
+// thin, is sliced only when the slices fill nine tenths of their workgroup
+// slots (B=72 H=12: one launch 163.8, 8 slices of 864 chunks 167.6; B=80 in 8
+// of 960: 181.7 / 172.6; B=56 in 7 of 768: 129.2 / 122.8).
 constexpr int64_t kSliceRound = 1024;
 constexpr int64_t kSliceCUs = 256;
 constexpr int64_t kSliceChain = 8;
+constexpr int64_t kSliceMax = 8;
 int64_t fwd_slices(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   const int64_t DG = group_width(v_dtype, D);
   if (B < 2 || DG != D || DG * elem_size(v_dtype) != 128) return 1;
@@ -2061,11 +2067,15 @@ int64_t fwd_slices(int64_t B, int64_t H, int64_t N, int64_t D, int v_dtype) {
   if (chain > kSliceChain || per_b > kSliceRound || B * per_b <= kSliceRound) return 1;
   const int64_t b_max = kSliceRound / per_b;
   const int64_t fewest = (B + b_max - 1) / b_max;
+  if (fewest > kSliceMax) return 1;
   int64_t best = fewest, best_rounds = 0;
-  for (int64_t n = fewest; n <= fewest + 2 && n <= B; ++n) {
+  for (int64_t n = fewest; n <= fewest + 2 && n <= B && n <= kSliceMax; ++n) {
     const int64_t rounds = n * (((B + n - 1) / n * per_b + kSliceCUs - 1) / kSliceCUs);
     if (n == fewest || rounds < best_rounds) best = n, best_rounds = rounds;
   }
+  const int64_t chunks = (B + best - 1) / best * per_b;
+  const int64_t slots = (chunks + kSliceCUs - 1) / kSliceCUs * kSliceCUs;
+  if (B * per_b >= 4 * kSliceRound && 10 * chunks < 9 * slots) return 1;
   return best;
 }
 

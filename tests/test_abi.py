@@ -96,6 +96,10 @@ def test_workspace_bytes(kdecay_lib):
     assert ws(40, 16, 4096, 64, _lib.KDECAY_BF16) == HDR + 8 * 16 * 8 * 64 * 8  # 5 of 1024
     assert ws(16, 12, 4096, 32, _lib.KDECAY_F32) == HDR + 8 * 12 * 8 * 32 * 8  # fp32 D=32: 8 + 8
     assert ws(128, 12, 512, 64, _lib.KDECAY_BF16) == 0  # 2 slices of single-chunk streams
+    assert ws(80, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 10 * 12 * 8 * 64 * 8  # 8 slices at most
+    assert ws(72, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 72 * 12 * 8 * 64 * 8  # 8 slices of 864: one launch
+    assert ws(56, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 8 * 12 * 8 * 64 * 8  # 7 slices of 768
+    assert ws(96, 12, 4096, 64, _lib.KDECAY_BF16) == HDR + 96 * 12 * 8 * 64 * 8  # more than 8 needed: one launch
     assert ws(14, 12, 4097, 64, _lib.KDECAY_BF16) == HDR + 14 * 12 * 9 * 64 * 8  # 9 per stream: one launch
     assert ws(3, 12, 8192, 64, _lib.KDECAY_BF16) == HDR + 3 * 12 * 16 * 64 * 8  # 16 per stream: one launch
     # At B=1, just above one resident round of 512-row chunks (8 or fewer per
