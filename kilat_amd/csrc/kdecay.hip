@@ -1098,7 +1098,9 @@ __device__ __forceinline__ void group_scan_rev(float (&acc)[VW], int gw, const f
   }
 }
 
-template <typename T, int LPR, int R, int NW, int W>
+// SL: a launch over a batch slice (kdecay_scan_bwd), whose head sums go
+// through BwdArgs::dlam_slices.
+template <typename T, int LPR, int R, int NW, int W, bool SL = false>
 struct ChunkBwd {
   static constexpr int VW = 16 / (int)sizeof(T);
   static constexpr int DG = LPR * VW;
@@ -1644,25 +1646,32 @@ struct ChunkBwd {
     }
     acc = wave_sum_f64(acc);
     if (lane == 0) {
-      if (a.slice + 1 < a.nslice) {
-        a.dlam_slices[(int64_t)a.slice * a.H + h] = acc;  // the last slice adds it
-      } else {
-        double t = acc;
-        if (a.slice > 0) {  // the earlier slices' sums in slice order, then this one's
-          t = a.dlam_slices[h];
-          for (int sl = 1; sl < a.slice; ++sl) t += a.dlam_slices[(int64_t)sl * a.H + h];
-          t += acc;
+      // Only the batch-slice kernels carry this (compiled into every kernel,
+      // it cost one more VGPR, and five waves per SIMD, in the 4-row
+      // narrow-group kernels and 1.2% at the B=8 N=4096 H=12 backward).
+      if constexpr (SL) {
+        if (a.slice + 1 < a.nslice) {
+          a.dlam_slices[(int64_t)a.slice * a.H + h] = acc;  // the last slice adds it
+        } else {
+          double t = acc;
+          if (a.slice > 0) {  // the earlier slices' sums in slice order, then this one's
+            t = a.dlam_slices[h];
+            for (int sl = 1; sl < a.slice; ++sl) t += a.dlam_slices[(int64_t)sl * a.H + h];
+            t += acc;
+          }
+          a.dlam[h] = (float)t;
         }
-        a.dlam[h] = (float)t;
+      } else {
+        a.dlam[h] = (float)acc;
       }
       if (!a.per_stream && !poisoned) count_done(a.hdr, (unsigned)a.ndone, epoch);
     }
   }
 };
 
-template <typename T, int LPR, int R, int NW, int W, int WPE>
+template <typename T, int LPR, int R, int NW, int W, int WPE, bool SL = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, 8))) void scan_bwd(BwdArgs a) {
-  using CB = ChunkBwd<T, LPR, R, NW, W>;
+  using CB = ChunkBwd<T, LPR, R, NW, W, SL>;
   __shared__ typename CB::Smem sm;
   CB::run(a, sm);
 }
@@ -2279,6 +2288,15 @@ int launch_bwd(const BwdArgs& a, int64_t grid, int R, hipStream_t s) {
   constexpr int VW = 16 / (int)sizeof(T);
   constexpr int LPR = DG / VW;
   if (R == kRB) {
+    // Batch slices (bwd_slices): one full round each, chains of at most 8.
+    if (a.nslice > 1) {
+      if constexpr (LPR == 8) {
+        hipLaunchKernelGGL((scan_bwd<T, LPR, kRB, kNWB, kW, 3, true>), dim3((unsigned)grid), dim3(kNWB * 64), 0, s, a);
+        return hip_check("scan_bwd launch");
+      } else {
+        return fail(KDECAY_ESHAPE, "no batch-slice backward kernel for %d-channel groups", DG);
+      }
+    }
     // One round: window 4, or 8 for chains of more than 8 chunks (a window
     // of 16 does not fit beside 16 rows per lane without spilling); several
     // rounds: 2.
