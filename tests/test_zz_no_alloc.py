@@ -49,7 +49,8 @@ def test_noalloc_matches_workspace_entry_point(hip_device, kdecay_lib):
     g = torch.Generator().manual_seed(60)
     # each call smaller than the previous one: the array keeps the larger
     # call's words and its epoch, which the next call must not take for its own
-    cases = [(8, 12, 4096, 64, torch.bfloat16, False), (2, 3, 1500, 64, torch.bfloat16, True),
+    cases = [(16, 12, 4096, 64, torch.bfloat16, True),  # two batch slices on the array, one after the other
+             (8, 12, 4096, 64, torch.bfloat16, False), (2, 3, 1500, 64, torch.bfloat16, True),
              (1, 4, 3000, 128, torch.float32, False), (1, 6, 2048, 64, torch.float64, True),
              (1, 2, 700, 32, torch.float16, True),
              (1, 1, 100, 64, torch.bfloat16, False)]
