@@ -314,6 +314,42 @@ def test_batch_slices(hip_device, kdecay_lib, dname, B, H, N, D, nslice):
         assert torch.equal(y32.to(dt), y)
 
 
+def test_batch_slices_replay_from_a_graph(hip_device, kdecay_lib):
+    """A batch-sliced scan (B=16 H=12 N=4096: two launches on one workspace)
+    captured in a HIP graph: each replay advances the epoch twice on the
+    device, with eager launches of another shape on the same workspace
+    between replays, and every replay equals the eager result bit for bit."""
+    g = torch.Generator().manual_seed(240)
+    lam = lam_uniform(12, 0.5, 0.9999, g).to(hip_device)
+    V = torch.randn(16, 12, 4096, 64, generator=g).to(torch.bfloat16).to(hip_device)
+    W = torch.randn(2, 12, 3000, 64, generator=g).to(torch.bfloat16).to(hip_device)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        y_ref, fin_ref = kilat_amd.global_decay_scan(lam, V, return_final_state=True)  # workspace made eagerly
+        w_ref = kilat_amd.global_decay_scan(lam, W)
+        y = torch.empty_like(y_ref)
+        fin = torch.empty_like(fin_ref)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            y2, fin2 = kilat_amd.global_decay_scan(lam, V, return_final_state=True)
+            y.copy_(y2)
+            fin.copy_(fin2)
+    torch.cuda.synchronize()
+    ref, sref = C.scan_f32(lam.cpu().numpy(), V.float().cpu().numpy(), None, 0)
+    assert_parity(y_ref.cpu(), torch.from_numpy(ref).to(torch.bfloat16), torch.bfloat16, "eager")
+    assert rel_err(fin_ref.cpu(), torch.from_numpy(sref)) <= 1e-5
+    for r in range(3):
+        print(f"  graph replay {r}", flush=True)
+        y.zero_(); fin.zero_()
+        with torch.cuda.stream(stream):
+            graph.replay()
+            w = kilat_amd.global_decay_scan(lam, W)
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_ref) and torch.equal(fin, fin_ref), r
+        assert torch.equal(w, w_ref), r
+
+
 def assert_same_rounding_as_fp32_output(lam, V, y, dev, ref32, what=""):
     """The scan with a 2-byte output gives bit for bit its own fp32 output
     rounded by torch (round-to-nearest-even): both are the same kernel's fp32
