@@ -420,8 +420,9 @@ def bench_forward_grids(torch, dev, steps=50):
     return out
 
 
-def bench_backward(torch, dev, steps=100):
-    """C2-shaped training pass: kdecay_scan_fwd_train, then kdecay_scan_bwd (dV, dlam).
+def bench_backward(torch, dev, steps=100, B=8, H=12):
+    """C2-shaped training pass (or another batch and head count at N=4096
+    D=64): kdecay_scan_fwd_train, then kdecay_scan_bwd (dV, dlam).
 
     Algorithmic bytes: forward 4 B/element (V in, y out); backward 6 B/element
     (V and gy in, dV out).  4 rotated buffer sets (400 MB of V and gy) keep the
@@ -430,7 +431,7 @@ def bench_backward(torch, dev, steps=100):
     from kilat_amd import _lib
     from kilat_amd.triton_ops import _stream_ptr, _workspace
 
-    B, H, N, D = 8, 12, 4096, 64
+    N, D = 4096, 64
     lib = _lib.load()
     code = _lib.KDECAY_BF16
     g = torch.Generator(device=dev).manual_seed(5)
@@ -471,7 +472,8 @@ def bench_backward(torch, dev, steps=100):
     if rc[0]:
         raise RuntimeError("training scan failed: " + lib.kdecay_last_error_string().decode())
     fus, bus = rf * 1e3 / steps, rb * 1e3 / steps
-    return {"config": "C2 shape, bf16: forward with saved states, then backward (dV, dlam)",
+    config = "C2 shape" if (B, H) == (8, 12) else f"B={B} H={H} N=4096 D=64"
+    return {"config": config + ", bf16: forward with saved states, then backward (dV, dlam)",
             "fwd_train_us": round(fus, 3), "fwd_train_GBps": round(4 * n / (fus * 1e-6) / 1e9, 1),
             "bwd_us": round(bus, 3), "bwd_GBps": round(6 * n / (bus * 1e-6) / 1e9, 1),
             "bwd_pct_of_peak": round(100 * 6 * n / (bus * 1e-6) / 1e9 / HBM_PEAK_GBPS, 2)}
@@ -801,6 +803,14 @@ def main() -> int:
         log("forward, grids of more than one round (bf16 D=64 N=4096)")
         extras["forward_grids"] = bench_forward_grids(torch, dev)
         torch.cuda.empty_cache()
+        # Backward grids of exactly two resident rounds, which the library runs
+        # as two batch slices: B=16 H=12, and the larger sample configuration's
+        # decay heads (H=16 of 64 channels) at B=12.
+        log("training pass, backward grids of two rounds (bf16 D=64 N=4096)")
+        extras["backward_grids"] = {}
+        for B2, H2 in ((16, 12), (12, 16)):
+            extras["backward_grids"][f"B{B2}_H{H2}"] = bench_backward(torch, dev, steps=50, B=B2, H=H2)
+            torch.cuda.empty_cache()
         log("end-to-end model forward (C5)")
         extras["e2e"] = bench_e2e(torch, dev)
     result["extras"] = extras
